@@ -1,0 +1,273 @@
+// C ABI entry points: argument validation, workspace carving, launches.
+// Every entry point is stream-ordered and allocates nothing.
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "g4_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, const char* detail = "") {
+  char buf[512];
+  snprintf(buf, sizeof buf, fmt, detail);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  char buf[512];
+  snprintf(buf, sizeof buf, "%s: HIP error %d (%s)", where, (int)e, hipGetErrorString(e));
+  g_last_error = buf;
+  return G4_ERR_LAUNCH;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int check_problem(const g4_problem* p) {
+  if (p == nullptr) return fail(G4_ERR_INVALID, "problem descriptor is NULL");
+  if (p->num_seqs < 1) return fail(G4_ERR_INVALID, "num_seqs must be >= 1");
+  if (p->num_q_heads < 1 || p->num_kv_heads < 1 || p->num_q_heads % p->num_kv_heads)
+    return fail(G4_ERR_INVALID, "num_q_heads must be a positive multiple of num_kv_heads");
+  if (p->head_dim != 256 && p->head_dim != 512)
+    return fail(G4_ERR_UNSUPPORTED, "head_dim must be 256 (local) or 512 (global)");
+  if (p->window < 0) return fail(G4_ERR_INVALID, "window must be >= 0");
+  if (p->seqlen_q < 1 || p->seqlen_k < 1)
+    return fail(G4_ERR_INVALID, "seqlen_q and seqlen_k must be >= 1");
+  if ((p->cu_seqlens_q == nullptr) != (p->cu_seqlens_k == nullptr))
+    return fail(G4_ERR_INVALID, "cu_seqlens_q and cu_seqlens_k must both be set or both NULL");
+  if (p->cu_seqlens_q == nullptr) {
+    if (p->seqlen_q > p->seqlen_k)
+      return fail(G4_ERR_INVALID, "fixed layout requires seqlen_q <= seqlen_k");
+  } else if (p->total_q < 1 || p->total_k < 1) {
+    return fail(G4_ERR_INVALID, "packed totals must be positive");
+  }
+  if ((int64_t)p->num_seqs * p->seqlen_q > 0x7fffffffLL ||
+      (int64_t)p->num_seqs * p->seqlen_k > 0x7fffffffLL)
+    return fail(G4_ERR_UNSUPPORTED, "token counts must fit int32");
+  return G4_OK;
+}
+
+int check_operand(const void* ptr, const g4_layout& l, const char* name) {
+  if (ptr == nullptr) return fail(G4_ERR_INVALID, "operand %s is NULL", name);
+  if (((uintptr_t)ptr) % 16) return fail(G4_ERR_INVALID, "operand %s must be 16-byte aligned", name);
+  if (l.token_stride <= 0 || l.head_stride <= 0 || l.token_stride % 8 || l.head_stride % 8 ||
+      l.batch_stride < 0 || l.batch_stride % 8)
+    return fail(G4_ERR_INVALID, "operand %s strides must be positive multiples of 8 elements",
+                name);
+  return G4_OK;
+}
+
+int check_ws(const g4_problem* p, int phase, void* ws, size_t bytes) {
+  size_t need = g4_workspace_bytes(p, phase);
+  if (bytes < need) {
+    char buf[128];
+    snprintf(buf, sizeof buf, "%zu bytes needed, %zu given", need, bytes);
+    return fail(G4_ERR_WORKSPACE, "workspace too small: %s", buf);
+  }
+  if (need > 0 && ws == nullptr) return fail(G4_ERR_WORKSPACE, "workspace is NULL");
+  if (((uintptr_t)ws) % 256) return fail(G4_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return G4_OK;
+}
+
+#define G4_TRY(expr)            \
+  do {                          \
+    int _rc = (expr);           \
+    if (_rc != G4_OK) return _rc; \
+  } while (0)
+
+// Workspace: [spans][delta]
+float* delta_ptr(const g4_problem& p, void* ws) {
+  return (float*)((char*)ws + align256(g4::spans_bytes(p)));
+}
+
+}  // namespace
+
+namespace g4 {
+size_t delta_bytes(const g4_problem& p) {
+  return align256((size_t)q_stream_tokens(p) * p.num_q_heads * 4);
+}
+}  // namespace g4
+
+extern "C" {
+
+int g4_abi_version(void) { return G4_ABI_VERSION; }
+
+const char* g4_last_error(void) { return g_last_error.c_str(); }
+
+size_t g4_workspace_bytes(const g4_problem* p, int phase) {
+  if (check_problem(p) != G4_OK) return 0;
+  size_t b = align256(g4::spans_bytes(*p));
+  if (phase == 1) b += g4::delta_bytes(*p);
+  return b;
+}
+
+int g4_attn_fwd(const g4_problem* p, const void* q, g4_layout ql, const void* k, g4_layout kl,
+                const void* v, g4_layout vl, void* o, g4_layout ol, float* lse, void* ws,
+                size_t ws_bytes, void* stream) {
+  G4_TRY(check_problem(p));
+  G4_TRY(check_operand(q, ql, "q"));
+  G4_TRY(check_operand(k, kl, "k"));
+  G4_TRY(check_operand(v, vl, "v"));
+  G4_TRY(check_operand(o, ol, "o"));
+  if (lse == nullptr) return fail(G4_ERR_INVALID, "lse is NULL");
+  G4_TRY(check_ws(p, 0, ws, ws_bytes));
+  hipStream_t st = (hipStream_t)stream;
+  g4::FwdParams a{};
+  a.p = *p;
+  a.q = (const __bf16*)q;
+  a.k = (const __bf16*)k;
+  a.v = (const __bf16*)v;
+  a.o = (__bf16*)o;
+  a.lse = lse;
+  a.ql = ql;
+  a.kl = kl;
+  a.vl = vl;
+  a.ol = ol;
+  a.num_seqs = p->num_seqs;
+  if (g4::spans_bytes(*p)) {
+    hipError_t e = g4::launch_spans(*p, ws, st);
+    if (e != hipSuccess) return hip_fail(e, "span table");
+  }
+  g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);
+  hipError_t e = g4::launch_fwd(a, st);
+  if (e != hipSuccess) return hip_fail(e, "forward");
+  return G4_OK;
+}
+
+static int fill_bwd(g4::BwdParams& a, const g4_problem* p, const void* q, g4_layout ql,
+                    const void* k, g4_layout kl, const void* v, g4_layout vl, void* ws) {
+  a.p = *p;
+  a.q = (const __bf16*)q;
+  a.k = (const __bf16*)k;
+  a.v = (const __bf16*)v;
+  a.ql = ql;
+  a.kl = kl;
+  a.vl = vl;
+  a.num_seqs = p->num_seqs;
+  a.delta = delta_ptr(*p, ws);
+  g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);
+  return G4_OK;
+}
+
+int g4_attn_bwd_delta(const g4_problem* p, const void* o, g4_layout ol, const void* dout,
+                      g4_layout dol, const float* dlse, void* ws, size_t ws_bytes, void* stream) {
+  G4_TRY(check_problem(p));
+  G4_TRY(check_operand(o, ol, "o"));
+  G4_TRY(check_operand(dout, dol, "dout"));
+  G4_TRY(check_ws(p, 1, ws, ws_bytes));
+  g4::BwdParams a{};
+  a.p = *p;
+  a.o = (const __bf16*)o;
+  a.dout = (const __bf16*)dout;
+  a.ol = ol;
+  a.dol = dol;
+  a.dlse = dlse;
+  a.num_seqs = p->num_seqs;
+  a.delta = delta_ptr(*p, ws);
+  hipStream_t st = (hipStream_t)stream;
+  if (g4::spans_bytes(*p)) {
+    hipError_t e = g4::launch_spans(*p, ws, st);
+    if (e != hipSuccess) return hip_fail(e, "span table");
+  }
+  hipError_t e = g4::launch_bwd_delta(a, st);
+  if (e != hipSuccess) return hip_fail(e, "backward delta");
+  return G4_OK;
+}
+
+int g4_attn_bwd_dkdv(const g4_problem* p, const void* q, g4_layout ql, const void* k,
+                     g4_layout kl, const void* v, g4_layout vl, const void* dout, g4_layout dol,
+                     const float* lse, void* dk, g4_layout dkl, void* dv, g4_layout dvl, void* ws,
+                     size_t ws_bytes, void* stream) {
+  G4_TRY(check_problem(p));
+  G4_TRY(check_operand(q, ql, "q"));
+  G4_TRY(check_operand(k, kl, "k"));
+  G4_TRY(check_operand(v, vl, "v"));
+  G4_TRY(check_operand(dout, dol, "dout"));
+  G4_TRY(check_operand(dk, dkl, "dk"));
+  G4_TRY(check_operand(dv, dvl, "dv"));
+  if (lse == nullptr) return fail(G4_ERR_INVALID, "lse is NULL");
+  G4_TRY(check_ws(p, 1, ws, ws_bytes));
+  g4::BwdParams a{};
+  fill_bwd(a, p, q, ql, k, kl, v, vl, ws);
+  a.dout = (const __bf16*)dout;
+  a.dol = dol;
+  a.lse = lse;
+  a.dk = (__bf16*)dk;
+  a.dv = (__bf16*)dv;
+  a.dkl = dkl;
+  a.dvl = dvl;
+  hipError_t e = g4::launch_bwd_dkdv(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "backward dK/dV");
+  return G4_OK;
+}
+
+int g4_attn_bwd_dq(const g4_problem* p, const void* q, g4_layout ql, const void* k, g4_layout kl,
+                   const void* v, g4_layout vl, const void* dout, g4_layout dol, const float* lse,
+                   void* dq, g4_layout dql, void* ws, size_t ws_bytes, void* stream) {
+  G4_TRY(check_problem(p));
+  G4_TRY(check_operand(q, ql, "q"));
+  G4_TRY(check_operand(k, kl, "k"));
+  G4_TRY(check_operand(v, vl, "v"));
+  G4_TRY(check_operand(dout, dol, "dout"));
+  G4_TRY(check_operand(dq, dql, "dq"));
+  if (lse == nullptr) return fail(G4_ERR_INVALID, "lse is NULL");
+  G4_TRY(check_ws(p, 1, ws, ws_bytes));
+  g4::BwdParams a{};
+  fill_bwd(a, p, q, ql, k, kl, v, vl, ws);
+  a.dout = (const __bf16*)dout;
+  a.dol = dol;
+  a.lse = lse;
+  a.dq = (__bf16*)dq;
+  a.dql = dql;
+  hipError_t e = g4::launch_bwd_dq(a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "backward dQ");
+  return G4_OK;
+}
+
+int g4_attn_bwd(const g4_problem* p, const void* q, g4_layout ql, const void* k, g4_layout kl,
+                const void* v, g4_layout vl, const void* o, g4_layout ol, const void* dout,
+                g4_layout dol, const float* lse, const float* dlse, void* dq, g4_layout dql,
+                void* dk, g4_layout dkl, void* dv, g4_layout dvl, void* ws, size_t ws_bytes,
+                void* stream) {
+  G4_TRY(g4_attn_bwd_delta(p, o, ol, dout, dol, dlse, ws, ws_bytes, stream));
+  G4_TRY(g4_attn_bwd_dkdv(p, q, ql, k, kl, v, vl, dout, dol, lse, dk, dkl, dv, dvl, ws, ws_bytes,
+                          stream));
+  G4_TRY(g4_attn_bwd_dq(p, q, ql, k, kl, v, vl, dout, dol, lse, dq, dql, ws, ws_bytes, stream));
+  return G4_OK;
+}
+
+int g4_mask_materialize(const g4_problem* p, uint8_t* out, void* ws, size_t ws_bytes,
+                        void* stream) {
+  G4_TRY(check_problem(p));
+  if (out == nullptr) return fail(G4_ERR_INVALID, "out is NULL");
+  (void)ws;
+  (void)ws_bytes;
+  hipError_t e = g4::launch_mask(*p, out, nullptr, nullptr, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "mask");
+  return G4_OK;
+}
+
+int g4_tile_ranges(const g4_problem* p, int direction, int row_tile, int32_t* out, void* ws,
+                   size_t ws_bytes, void* stream) {
+  G4_TRY(check_problem(p));
+  if (out == nullptr) return fail(G4_ERR_INVALID, "out is NULL");
+  if (direction != 0 && direction != 1) return fail(G4_ERR_INVALID, "direction must be 0 or 1");
+  if (row_tile < 1 || row_tile > 1024) return fail(G4_ERR_INVALID, "row_tile must be in [1, 1024]");
+  G4_TRY(check_ws(p, 0, ws, ws_bytes));
+  hipStream_t st = (hipStream_t)stream;
+  if (g4::spans_bytes(*p)) {
+    hipError_t e = g4::launch_spans(*p, ws, st);
+    if (e != hipSuccess) return hip_fail(e, "span table");
+  }
+  const int *lo, *hi;
+  g4::span_arrays(*p, ws, &lo, &hi);
+  hipError_t e = g4::launch_ranges(*p, direction, row_tile, out, lo, hi, st);
+  if (e != hipSuccess) return hip_fail(e, "ranges");
+  return G4_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,301 @@
+// Shared device-side building blocks of the gfx950 Gemma 4 attention kernels.
+//
+// Conventions (all kernels):
+//  * MFMA v_mfma_f32_32x32x16_bf16 (64 lanes).  For C[32 x 32] += A[32 x 16] B[16 x 32]:
+//      A: lane l holds row (l & 31), k = 8*(l >> 5) + 0..7
+//      B: lane l holds col (l & 31), k = 8*(l >> 5) + 0..7
+//      C: lane l, register r holds row 8*(r >> 2) + 4*(l >> 5) + (r & 3), col (l & 31)
+//  * Reduction-dimension permutation: when an accumulator tile is reused as an
+//    MFMA operand, the 16 k-values an MFMA consumes are taken from accumulator
+//    registers 8m..8m+7, i.e. rows {16m' + 4h + e, 16m' + 8 + 4h + e : e < 4}
+//    for lane half h.  The matching operand is read with two transposing LDS
+//    reads (ds_read_b64_tr_b16), one per 4-row group, so no data is permuted
+//    in memory.
+//  * LDS tiles hold rows of 16-byte chunks; chunk c of row r is stored at slot
+//    c ^ swz(r) with swz(r) = 4*(r & 3) + ((r >> 2) & 3), which keeps both the
+//    row-wise 16-byte MFMA operand reads and the 4-row transposing reads free of
+//    bank conflicts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemma4_attn.h"
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+#define G4_LDS __attribute__((address_space(3)))
+
+namespace g4 {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Swizzled 16-byte slot of chunk c in row r.
+__device__ __forceinline__ int swz_slot(int r, int c) {
+  return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
+}
+
+// Byte offset of element (row r, column col) of a bf16 LDS tile whose rows
+// hold `row_chunks` 16-byte chunks.  col must be a multiple of 4 (8-byte
+// accesses) -- the 8-byte half within the chunk is preserved.
+__device__ __forceinline__ int lds_off(int r, int col, int row_chunks) {
+  int c = col >> 3;
+  return (r * row_chunks + swz_slot(r, c)) * 16 + (col & 7) * 2;
+}
+
+__device__ __forceinline__ bf16x8 lds_read16(const char G4_LDS* base, int off) {
+  return *(const bf16x8 G4_LDS*)(base + off);
+}
+
+__device__ __forceinline__ bf16x4 lds_read_tr(const char G4_LDS* base, int off) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((bf16x4 G4_LDS*)(base + off));
+}
+
+__device__ __forceinline__ bf16x8 cat4(bf16x4 a, bf16x4 b) {
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Async 16-byte global -> LDS copy: lane l writes LDS bytes [base + 16 l, +16).
+__device__ __forceinline__ void g2l16(const void* gptr, char G4_LDS* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(gptr, (void G4_LDS*)lds_wave_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 ld_global16(const void* p) {
+  return *(const bf16x8*)p;
+}
+
+__device__ __forceinline__ float wave_xor32(float x) { return __shfl_xor(x, 32, 64); }
+
+// Workgroup barrier that orders LDS traffic only.  Unlike __syncthreads() it
+// does not drain outstanding global loads, so tile copies issued earlier stay
+// in flight across it; callers wait for those with vm_wait<N>() first.
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Async 4-byte global -> LDS copy: lane l writes LDS bytes [base + 4 l, +4).
+__device__ __forceinline__ void g2l4(const void* gptr, char G4_LDS* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(gptr, (void G4_LDS*)lds_wave_base, 4, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Per-lane LDS offsets for row-wise 16-byte MFMA operand reads of a swizzled
+// tile with CPR chunks per row: lane reads row (row0 + (lane & 31)) and chunk
+// (cbase + 2 c' + (lane >> 5)), c' < 8 * n, row0 and cbase multiples of 16.
+// The XOR of the swizzle only touches the low 4 chunk bits, so the offset
+// splits into one of 8 per-lane registers plus a compile-time immediate.
+template <int CPR>
+struct RowReader {
+  int off[8];
+  __device__ __forceinline__ void init(int lane) {
+    const int r = lane & 31, h = lane >> 5;
+    const int sw = ((r & 3) << 2) | ((r >> 2) & 3);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) off[w] = (r * CPR + ((2 * w + h) ^ sw)) * 16;
+  }
+  template <int ROW0, int CBASE, int CP>
+  __device__ __forceinline__ bf16x8 read(const char G4_LDS* tile) const {
+    static_assert(ROW0 % 16 == 0 && CBASE % 16 == 0, "alignment");
+    return *(const bf16x8 G4_LDS*)(tile + off[CP & 7] + (ROW0 * CPR + CBASE + 16 * (CP >> 3)) * 16);
+  }
+};
+
+// Per-lane LDS offsets for the transposing reads that build a 32 x 16 MFMA A
+// operand (rows = 32 columns of the tile starting at chunk cbase + 4 b, k = 16
+// tile rows starting at row0) from a row-major swizzled tile:
+// lane l gets column 16*((l>>4)&1) + (l&15) and rows {4h + e, 8 + 4h + e}.
+template <int CPR>
+struct TrReader {
+  int off[2][4];
+  __device__ __forceinline__ void init(int lane) {
+    const int g = lane >> 4, sl = lane & 15;
+    const int rl = 4 * (g >> 1) + (sl >> 2);
+    const int lb = 2 * (g & 1) + ((sl >> 1) & 1);
+    const int half = (sl & 1) * 8;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int r = rl + 8 * e;
+      const int sw = ((r & 3) << 2) | ((r >> 2) & 3);
+#pragma unroll
+      for (int bq = 0; bq < 4; ++bq) off[e][bq] = (r * CPR + ((4 * bq + lb) ^ sw)) * 16 + half;
+    }
+  }
+  template <int ROW0, int CBASE, int B>
+  __device__ __forceinline__ bf16x8 read(const char G4_LDS* tile) const {
+    static_assert(ROW0 % 16 == 0 && CBASE % 16 == 0, "alignment");
+    constexpr int imm = (ROW0 * CPR + CBASE + 16 * (B >> 2)) * 16;
+    bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (bf16x4 G4_LDS*)(tile + off[0][B & 3] + imm));
+    bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (bf16x4 G4_LDS*)(tile + off[1][B & 3] + imm));
+    return cat4(lo, hi);
+  }
+};
+
+// Async copy of a BN-row tile of a row-major operand (rows of CPR 16-byte
+// chunks) into a swizzled LDS tile by NW waves.  Per-lane byte offsets of the
+// chunks relative to the tile's first row are precomputed; the tile base is a
+// wave-uniform pointer.
+template <int CPR, int BN, int NW>
+struct TileCopier {
+  static constexpr int kPer = BN * CPR / (64 * NW);
+  static_assert(kPer * 64 * NW == BN * CPR, "tile must split evenly over the waves");
+  uint32_t goff[kPer];  // byte offset of this lane's chunk i
+  int lds_wave;         // byte offset of this wave's first chunk slot
+  __device__ __forceinline__ void init(int64_t row_stride_elems, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int p = (i * NW + wave) * 64 + lane;
+      const int r = p / CPR;
+      const int c = (p % CPR) ^ (((r & 3) << 2) | ((r >> 2) & 3));
+      goff[i] = (uint32_t)(r * row_stride_elems * 2 + c * 16);
+    }
+    lds_wave = __builtin_amdgcn_readfirstlane(wave * 64 * 16);
+  }
+  // rows row0 .. row0 + BN - 1 must all exist.
+  __device__ __forceinline__ void issue(const __bf16* tile_row0, char G4_LDS* tile) const {
+    const char* g = (const char*)tile_row0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      g2l16(g + goff[i], tile + lds_wave + i * NW * 64 * 16);
+  }
+  // Tail tile: rows >= nrows are replaced by row nrows - 1 (their scores are
+  // masked, so they only need to be finite data).
+  __device__ __forceinline__ void issue_clamped(const __bf16* tile_row0, int64_t row_stride_elems,
+                                                int nrows, char G4_LDS* tile, int wave,
+                                                int lane) const {
+    const char* g = (const char*)tile_row0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int p = (i * NW + wave) * 64 + lane;
+      const int r = p / CPR;
+      const int c = (p % CPR) ^ (((r & 3) << 2) | ((r >> 2) & 3));
+      const int64_t off = (int64_t)min(r, nrows - 1) * row_stride_elems * 2 + c * 16;
+      g2l16(g + off, tile + lds_wave + i * NW * 64 * 16);
+    }
+  }
+};
+
+// Scheduling hint for a region of N MFMAs fed by LDS reads: PRE reads first,
+// then (1 MFMA, PER reads) repeated, so only a few operand fragments are in
+// flight at any time (the default schedule hoists every read to the top of
+// the region and runs out of VGPRs).  Place it at the end of the region,
+// which must be delimited by sched_barrier(0).
+template <int N, int PRE, int PER>
+__device__ __forceinline__ void mfma_pipeline_hint() {
+  __builtin_amdgcn_sched_group_barrier(0x100, PRE, 0);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);
+  }
+}
+
+// Sequence geometry resolved from a problem (fixed or packed).
+struct Seq {
+  int lq, lk;          // lengths
+  int64_t qtok, ktok;  // token index of the sequence start in the Q / K stream
+  int64_t q_off_b, k_off_b;  // fixed mode: element offsets of the batch
+  bool packed;
+};
+
+__device__ __forceinline__ Seq resolve_seq(const g4_problem& p, int s) {
+  Seq r;
+  r.packed = p.cu_seqlens_q != nullptr;
+  if (r.packed) {
+    int q0 = p.cu_seqlens_q[s], q1 = p.cu_seqlens_q[s + 1];
+    int k0 = p.cu_seqlens_k[s], k1 = p.cu_seqlens_k[s + 1];
+    r.lq = q1 - q0;
+    r.lk = k1 - k0;
+    r.qtok = q0;
+    r.ktok = k0;
+  } else {
+    r.lq = p.seqlen_q;
+    r.lk = p.seqlen_k;
+    r.qtok = (int64_t)s * p.seqlen_q;
+    r.ktok = (int64_t)s * p.seqlen_k;
+  }
+  return r;
+}
+
+// Element offset of token t (sequence-local) of sequence s in an operand.
+__device__ __forceinline__ int64_t tok_off(const Seq& sq, int s, int64_t seq_tok0, int t,
+                                           const g4_layout& L) {
+  return sq.packed ? (seq_tok0 + t) * L.token_stride
+                   : (int64_t)s * L.batch_stride + (int64_t)t * L.token_stride;
+}
+
+// LSE / delta element offset for (s, h, local token i).
+__device__ __forceinline__ int64_t lse_off(const g4_problem& p, const Seq& sq, int s, int h,
+                                           int i) {
+  return (sq.packed ? sq.qtok : (int64_t)s * p.lse_batch_stride) +
+         (int64_t)h * p.lse_head_stride + i;
+}
+
+// The Gemma predicate for query at K-position a and key j of one sequence.
+__device__ __forceinline__ bool allowed(int a, int j, int window, bool bidir, int vq, int vk,
+                                        bool use_doc, int dq, int dk) {
+  bool keep = (j <= a) || (bidir && vq >= 0 && vq == vk);
+  if (window > 0) keep = keep && (j > a - window);
+  if (use_doc) keep = keep && (dq == dk);
+  return keep;
+}
+
+// Key range [lo, hi) (sequence-local key indices) a tile of queries whose
+// K-positions are [a0, a1] may attend to, given the maximum span end of its
+// vision queries (span_hi_max, -1 if none).
+__device__ __forceinline__ void query_tile_key_range(int a0, int a1, int lk, int window,
+                                                     int span_hi_max, int& lo, int& hi) {
+  lo = window > 0 ? max(0, a0 - window + 1) : 0;
+  hi = max(a1, span_hi_max) + 1;
+  hi = min(hi, lk);
+}
+
+// Query range [lo, hi) (sequence-local query indices) a tile of keys [j0, j1]
+// may be attended by, given the minimum span start of its vision keys
+// (span_lo_min, large if none).  off = Sk - Sq.
+__device__ __forceinline__ void key_tile_query_range(int j0, int j1, int lq, int off, int window,
+                                                     int span_lo_min, int& lo, int& hi) {
+  int a_lo = min(j0, span_lo_min);
+  int a_hi = window > 0 ? j1 + window - 1 : 0x7fffffff - 1;
+  lo = max(0, a_lo - off);
+  hi = min(lq, a_hi - off + 1);
+  if (hi < lo) hi = lo;
+}
+
+// Map the hardware block index onto a logical work index so that each XCD
+// (blocks are dealt round-robin over 8 XCDs) receives a contiguous run of
+// logical work items.  Bijective for any grid size.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  constexpr int kXcd = 8;
+  int xcd = bid % kXcd, pos = bid / kXcd;
+  int base = nblocks / kXcd, extra = nblocks % kXcd;
+  return xcd * base + min(xcd, extra) + pos;
+}
+
+// Tile rank -> tile index alternating from the heaviest (last) tile:
+// n-1, 0, n-2, 1, ...
+__device__ __forceinline__ int zigzag(int r, int n) {
+  return (r & 1) ? (r >> 1) : (n - 1 - (r >> 1));
+}
+
+}  // namespace g4

@@ -1,0 +1,416 @@
+// Forward attention kernel for gfx950: O = softmax(Q K^T + mask) V, fp32 LSE.
+//
+// One workgroup owns BM = 32 * NQG queries of one query head and walks the key
+// tiles its mask-aware range admits (query_tile_key_range).  Each wave owns
+// 32 queries and a DH = D / DSPLIT slice of the head dimension:
+//   S^T (keys x queries) = K Q^T on MFMA with the query fragments in VGPRs and
+//   K read from LDS; with DSPLIT = 2 the two d-slices of a query group
+//   exchange their partial S^T through LDS and add them.  Because lanes own
+//   queries, the softmax row max / sum are register reductions plus one
+//   cross-half shuffle.  P is rounded to bf16 and fed straight from the
+//   accumulator registers as the B operand of O^T += V^T P^T, with V^T read
+//   from the natural-layout V tile by transposing LDS reads.
+// K and V tiles are copied global -> LDS asynchronously (one 16-byte chunk per
+// lane) one tile ahead of the compute.
+#include "g4_kernels.h"
+
+namespace g4 {
+
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE>
+struct FwdCfg {
+  static constexpr int kNW = NQG * DSPLIT;
+  static constexpr int kNT = kNW * 64;
+  static constexpr int kBM = NQG * 32;
+  static constexpr int kDH = D / DSPLIT;
+  static constexpr int kCPR = D / 8;  // 16-byte chunks per row
+  static constexpr int kTileBytes = BN * D * 2;
+  static constexpr int kLoadsPerWave = BN * kCPR / (64 * kNW);
+  static constexpr int kKB = BN / 32;  // 32-key blocks per tile
+  static constexpr int kXBytes = DSPLIT > 1 ? kNW * kKB * 4096 : 0;
+  static constexpr int kVBufs = VDOUBLE ? 2 : 1;
+  static constexpr int kLdsK = 0;
+  static constexpr int kLdsV = kLdsK + 2 * kTileBytes;
+  static constexpr int kLdsX = kLdsV + kVBufs * kTileBytes;
+  static constexpr int kLdsMeta = kLdsX + kXBytes;  // [buf][vid x 64 | doc x 64] int32
+  static constexpr int kLdsRed = kLdsMeta + 2 * 512;
+  static constexpr int kLdsBytes = kLdsRed + 16 * 4;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+  static_assert(kDH % 128 == 0, "head-dim slice must be a multiple of 128");
+};
+
+// Async copy of the vision / document IDs of keys [j0, j0 + 64) of a sequence
+// (clamped to its last key; keys past the end are masked by index).
+__device__ __forceinline__ void issue_meta(const g4_problem& p, const Seq& sq, int j0,
+                                           char G4_LDS* dst, int lane) {
+  const int64_t idx = sq.ktok + min(j0 + lane, sq.lk - 1);
+  if (p.vision_ids != nullptr && p.bidirectional_vision) g2l4(p.vision_ids + idx, dst);
+  if (p.document_ids != nullptr) g2l4(p.document_ids + idx, dst + 256);
+}
+
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META>
+struct FwdKernel {
+  using C = FwdCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
+  static constexpr int kNB = C::kDH / 32;  // 32-wide head-dim blocks per wave
+  static constexpr int kNC = C::kDH / 16;  // 16-deep head-dim steps per wave
+
+  char G4_LDS* smem;
+  const g4_problem* p;
+  Seq sq;
+  int tid, lane, wave, dh, h32;
+  int my_a, my_vid, my_doc;
+  bool has_vid, has_doc, has_meta;
+  int a0;
+  const __bf16* kbase;
+  const __bf16* vbase;
+  int64_t kstride, vstride;
+  RowReader<C::kCPR> krd;
+  TrReader<C::kCPR> vrd;
+  TileCopier<C::kCPR, BN, C::kNW> kcp, vcp;
+  bf16x8 qf[kNC];
+  f32x16 o_acc[kNB];
+  float m_run, l_run;
+
+  __device__ __forceinline__ void issue_k(int row0, int buf) {
+    char G4_LDS* dst = smem + C::kLdsK + buf * C::kTileBytes;
+    if (row0 + BN <= sq.lk)
+      kcp.issue(kbase + row0 * kstride, dst);
+    else
+      kcp.issue_clamped(kbase + row0 * kstride, kstride, sq.lk - row0, dst, wave, lane);
+  }
+  __device__ __forceinline__ void issue_v(int row0, int buf) {
+    char G4_LDS* dst = smem + C::kLdsV + buf * C::kTileBytes;
+    if (row0 + BN <= sq.lk)
+      vcp.issue(vbase + row0 * vstride, dst);
+    else
+      vcp.issue_clamped(vbase + row0 * vstride, vstride, sq.lk - row0, dst, wave, lane);
+  }
+
+  template <int KB, int CP>
+  __device__ __forceinline__ void s_step(const char G4_LDS* kt, f32x16& acc) const {
+    if constexpr (CP < kNC) {
+      // slice dh starts at chunk dh * kDH / 8 (a multiple of 16)
+      bf16x8 kf = krd.template read<KB * 32, 0, CP>(kt + dh * C::kDH * 2);
+      acc = mfma32(kf, qf[CP], acc);
+      s_step<KB, CP + 1>(kt, acc);
+    }
+  }
+
+  template <int KB, int HK, int B>
+  __device__ __forceinline__ void pv_step(const char G4_LDS* vt, const bf16x8& pb) {
+    if constexpr (B < kNB) {
+      bf16x8 vf = vrd.template read<KB * 32 + 16 * HK, 0, B>(vt + dh * C::kDH * 2);
+      o_acc[B] = mfma32(vf, pb, o_acc[B]);
+      pv_step<KB, HK, B + 1>(vt, pb);
+    }
+  }
+
+  // Branch-free Gemma predicate on the lane's 16 * kKB scores (keys kb0 + ...).
+  // Causal part: lo_w <= j <= min(a, Sk - 1); vision part: same non-negative
+  // block, j >= lo_w, j < Sk; document part: equal IDs.
+  template <int CUR>
+  __device__ __forceinline__ void apply_mask(f32x16 (&sacc)[C::kKB], int kb0) const {
+    const int lo_w = p->window > 0 ? my_a - p->window + 1 : -0x40000000;
+    const int hi_c = min(my_a, sq.lk - 1);
+    const int* km = (const int*)(smem + C::kLdsMeta + CUR * 512);
+#pragma unroll
+    for (int kb = 0; kb < C::kKB; ++kb)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int jl0 = kb * 32 + 8 * r4 + 4 * h32;
+        i32x4 vk = {-1, -1, -1, -1}, dk = {0, 0, 0, 0};
+        if (has_meta) {
+          vk = *(const i32x4*)(km + jl0);
+          dk = *(const i32x4*)(km + 64 + jl0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = kb0 + jl0 + e;
+          const bool in_w = j >= lo_w;
+          const bool causal = in_w & (j <= hi_c);
+          const bool vis = has_vid & (my_vid >= 0) & (vk[e] == my_vid) & in_w & (j < sq.lk);
+          const bool doc_ok = !has_doc | (dk[e] == my_doc);
+          const bool ok = (causal | vis) & doc_ok;
+          sacc[kb][r4 * 4 + e] = ok ? sacc[kb][r4 * 4 + e] : kNegInf;
+        }
+      }
+  }
+
+  template <int CUR>
+  __device__ __forceinline__ void step(int it, int ntiles, int t_first) {
+    const int kb0 = (t_first + it) * BN;
+    // This wave's copies of K (and, double-buffered, V) for this tile have
+    // landed; the barrier publishes every wave's copies and ends all reads of
+    // the buffers refilled below.
+    if constexpr (VDOUBLE)
+      vm_wait<0>();
+    else
+      vm_wait<C::kLoadsPerWave>();
+    barrier_lds();
+    if (it + 1 < ntiles) {
+      issue_k(kb0 + BN, CUR ^ 1);
+      if (has_meta && wave == 0) issue_meta(*p, sq, kb0 + BN, smem + C::kLdsMeta + (CUR ^ 1) * 512, lane);
+      if constexpr (VDOUBLE) issue_v(kb0 + BN, CUR ^ 1);
+    }
+
+    // S^T partial over this wave's head-dim slice.
+    f32x16 sacc[C::kKB];
+    const char G4_LDS* kt = smem + C::kLdsK + CUR * C::kTileBytes;
+    __builtin_amdgcn_sched_barrier(0);
+    sacc[0] = f32x16{};
+    s_step<0, 0>(kt, sacc[0]);
+    if constexpr (C::kKB > 1) {
+      sacc[1] = f32x16{};
+      s_step<1, 0>(kt, sacc[1]);
+    }
+    mfma_pipeline_hint<C::kKB * kNC, 3, 1>();
+
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (DSPLIT > 1) {
+      // Publish the partial, then add the partner slice's partial.
+      char G4_LDS* xb = smem + C::kLdsX;
+#pragma unroll
+      for (int kb = 0; kb < C::kKB; ++kb)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          f32x4 v = {sacc[kb][q4 * 4], sacc[kb][q4 * 4 + 1], sacc[kb][q4 * 4 + 2],
+                     sacc[kb][q4 * 4 + 3]};
+          *(f32x4 G4_LDS*)(xb + (((wave * C::kKB + kb) * 4 + q4) * 64 + lane) * 16) = v;
+        }
+      // Single V buffer: this tile's V copies were issued after the previous
+      // PV phase, before the K copies of the next tile.
+      if constexpr (!VDOUBLE) vm_wait<C::kLoadsPerWave>();
+      barrier_lds();
+      const int pw = wave ^ 1;
+#pragma unroll
+      for (int kb = 0; kb < C::kKB; ++kb)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          f32x4 v =
+              *(const f32x4 G4_LDS*)(xb + (((pw * C::kKB + kb) * 4 + q4) * 64 + lane) * 16);
+          // add in slice order so both slices hold bit-identical scores
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float mine = sacc[kb][q4 * 4 + e];
+            sacc[kb][q4 * 4 + e] = dh == 0 ? mine + v[e] : v[e] + mine;
+          }
+        }
+    } else if constexpr (!VDOUBLE) {
+      vm_wait<C::kLoadsPerWave>();
+      barrier_lds();
+    }
+
+    // Mask (only on tiles the mask does not fully admit), then online softmax
+    // in the log2 domain (softmax scale is 1.0).
+    const bool full = !has_doc && (kb0 + BN <= sq.lk) && (kb0 + BN - 1 <= a0) &&
+                      (p->window <= 0 || kb0 > a0 + C::kBM - 1 - p->window);
+#pragma unroll
+    for (int kb = 0; kb < C::kKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[kb][r] *= kLog2e;
+    if (!full) apply_mask<CUR>(sacc, kb0);
+    float mx = kNegInf;
+#pragma unroll
+    for (int kb = 0; kb < C::kKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+    mx = fmaxf(mx, wave_xor32(mx));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    float rs = 0.f;
+    bf16x8 pb[C::kKB][2];
+#pragma unroll
+    for (int kb = 0; kb < C::kKB; ++kb)
+#pragma unroll
+      for (int hk = 0; hk < 2; ++hk)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          float pv = fast_exp2(sacc[kb][hk * 8 + m] - m_use);
+          rs += pv;
+          pb[kb][hk][m] = (__bf16)pv;
+        }
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int b = 0; b < kNB; ++b) o_acc[b] *= alpha;
+    }
+
+    // O^T += V^T P^T with V^T from transposing reads of the V tile.
+    const char G4_LDS* vt = smem + C::kLdsV + (VDOUBLE ? CUR : 0) * C::kTileBytes;
+    __builtin_amdgcn_sched_barrier(0);
+    pv_step<0, 0, 0>(vt, pb[0][0]);
+    pv_step<0, 1, 0>(vt, pb[0][1]);
+    if constexpr (C::kKB > 1) {
+      pv_step<1, 0, 0>(vt, pb[1][0]);
+      pv_step<1, 1, 0>(vt, pb[1][1]);
+    }
+    mfma_pipeline_hint<C::kKB * 2 * kNB, 6, 2>();
+
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!VDOUBLE) {
+      // Single V buffer: every wave must finish its PV reads before refill.
+      barrier_lds();
+      if (it + 1 < ntiles) issue_v(kb0 + BN, 0);
+    }
+  }
+};
+
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META>
+__global__ void __launch_bounds__(NQG * DSPLIT * 64, 1) fwd_kernel(FwdParams a) {
+  using K = FwdKernel<D, BN, DSPLIT, NQG, VDOUBLE, META>;
+  using C = typename K::C;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  K ker;
+  ker.smem = (char G4_LDS*)smem_raw;
+  ker.p = &a.p;
+  const g4_problem& p = a.p;
+
+  ker.tid = threadIdx.x;
+  ker.lane = ker.tid & 63;
+  ker.wave = __builtin_amdgcn_readfirstlane(ker.tid >> 6);
+  const int qg = ker.wave / DSPLIT;
+  ker.dh = ker.wave % DSPLIT;
+  ker.h32 = ker.lane >> 5;
+  const int l32 = ker.lane & 31;
+
+  // ---- work item -------------------------------------------------------
+  const int grp = p.num_q_heads / p.num_kv_heads;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_kvh = a.num_seqs * a.ntq * grp;
+  const int kvh = L / per_kvh;
+  const int rem = L % per_kvh;
+  const int rank = rem / grp;
+  const int qh = kvh * grp + rem % grp;
+  const int s = rank / a.ntq;
+  const int qt = zigzag(rank % a.ntq, a.ntq);
+
+  ker.sq = resolve_seq(p, s);
+  const Seq& sq = ker.sq;
+  const int i0 = qt * C::kBM;
+  if (i0 >= sq.lq) return;
+  const int off = sq.lk - sq.lq;  // query i sits at key position i + off
+  ker.a0 = i0 + off;
+  const int a_last_valid = min(i0 + C::kBM, sq.lq) - 1 + off;
+  ker.has_vid = META && p.vision_ids != nullptr && p.bidirectional_vision;
+  ker.has_doc = META && p.document_ids != nullptr;
+  ker.has_meta = ker.has_vid || ker.has_doc;
+
+  // ---- key range (mask-aware tile scheduler) -------------------------------
+  int span_max = -1;
+  if (ker.has_vid) {
+    int* red = (int*)(smem_raw + C::kLdsRed);
+    int v = -1;
+    for (int t = ker.tid; t < C::kBM; t += C::kNT) {
+      int i = i0 + t;
+      if (i < sq.lq) v = max(v, a.span_hi[sq.ktok + i + off]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+    if (ker.lane == 0) red[ker.wave] = v;
+    barrier_lds();
+#pragma unroll
+    for (int w = 0; w < C::kNW; ++w) span_max = max(span_max, red[w]);
+  }
+  int klo, khi;
+  query_tile_key_range(ker.a0, a_last_valid, sq.lk, p.window, span_max, klo, khi);
+  const int t_first = klo / BN;
+  const int ntiles = (khi + BN - 1) / BN - t_first;
+
+  // ---- operand bases, address tables ---------------------------------------
+  ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
+  ker.vbase = a.v + tok_off(sq, s, sq.ktok, 0, a.vl) + (int64_t)kvh * a.vl.head_stride;
+  ker.kstride = a.kl.token_stride;
+  ker.vstride = a.vl.token_stride;
+  ker.krd.init(ker.lane);
+  ker.vrd.init(ker.lane);
+  ker.kcp.init(ker.kstride, ker.wave, ker.lane);
+  ker.vcp.init(ker.vstride, ker.wave, ker.lane);
+
+  // ---- query fragments (B operand of S^T = K Q^T) -------------------------
+  const int my_i = i0 + qg * 32 + l32;  // this lane's query
+  ker.my_a = my_i + off;
+  const bool q_valid = my_i < sq.lq;
+  {
+    const __bf16* qrow = a.q + tok_off(sq, s, sq.qtok, min(my_i, sq.lq - 1), a.ql) +
+                         (int64_t)qh * a.ql.head_stride + ker.dh * C::kDH + ker.h32 * 8;
+#pragma unroll
+    for (int c = 0; c < K::kNC; ++c) {
+      bf16x8 x = ld_global16(qrow + c * 16);
+      ker.qf[c] = q_valid ? x : bf16x8{};
+    }
+  }
+  ker.my_vid = -1;
+  ker.my_doc = 0;
+  if (ker.has_vid && q_valid) ker.my_vid = p.vision_ids[sq.ktok + ker.my_a];
+  if (ker.has_doc && q_valid) ker.my_doc = p.document_ids[sq.ktok + ker.my_a];
+
+  // ---- prologue: tile 0 (issue order K, key metadata, V) -----------------
+  if (ntiles > 0) {
+    ker.issue_k(t_first * BN, 0);
+    if (ker.has_meta && ker.wave == 0) issue_meta(p, sq, t_first * BN, ker.smem + C::kLdsMeta, ker.lane);
+    ker.issue_v(t_first * BN, 0);
+  }
+
+#pragma unroll
+  for (int b = 0; b < K::kNB; ++b) ker.o_acc[b] = f32x16{};
+  ker.m_run = kNegInf;
+  ker.l_run = 0.f;
+
+  for (int it = 0; it < ntiles; it += 2) {
+    ker.template step<0>(it, ntiles, t_first);
+    if (it + 1 < ntiles) ker.template step<1>(it + 1, ntiles, t_first);
+  }
+
+  // ---- epilogue: normalise, write O and LSE ---------------------------------
+  const float l_tot = ker.l_run + wave_xor32(ker.l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (q_valid) {
+    __bf16* orow = a.o + tok_off(sq, s, sq.qtok, my_i, a.ol) + (int64_t)qh * a.ol.head_stride;
+#pragma unroll
+    for (int b = 0; b < K::kNB; ++b) {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = ker.dh * C::kDH + b * 32 + 8 * r4 + 4 * ker.h32;
+        const f32x16& acc = ker.o_acc[b];
+        bf16x4 v = {(__bf16)(acc[r4 * 4] * inv), (__bf16)(acc[r4 * 4 + 1] * inv),
+                    (__bf16)(acc[r4 * 4 + 2] * inv), (__bf16)(acc[r4 * 4 + 3] * inv)};
+        *(bf16x4*)(orow + d) = v;
+      }
+    }
+    if (ker.dh == 0 && ker.h32 == 0) {
+      a.lse[lse_off(p, sq, s, qh, my_i)] =
+          l_tot > 0.f ? (ker.m_run + fast_log2(l_tot)) * kLn2 : kNegInf;
+    }
+  }
+}
+
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE>
+static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream) {
+  using C = FwdCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
+  const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
+                    a.p.document_ids != nullptr;
+  auto kern = meta ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, true>
+                   : fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false>;
+  static bool attr_set[2] = {false, false};
+  if (!attr_set[meta]) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+    if (e != hipSuccess) return e;
+    attr_set[meta] = true;
+  }
+  FwdParams b = a;
+  b.ntq = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
+  const int64_t nblocks = (int64_t)b.num_seqs * b.ntq * a.p.num_q_heads;
+  if (nblocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
+  return hipGetLastError();
+}
+
+hipError_t launch_fwd(const FwdParams& a, hipStream_t stream) {
+  if (a.p.head_dim == 256) return launch_fwd_cfg<256, 64, 1, 4, true>(a, stream);
+  if (a.p.head_dim == 512) return launch_fwd_cfg<512, 32, 2, 2, true>(a, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace g4

@@ -1,0 +1,59 @@
+// Kernel parameter blocks and launchers shared by the C ABI layer.
+#pragma once
+
+#include "g4_common.h"
+
+namespace g4 {
+
+struct FwdParams {
+  g4_problem p;
+  const __bf16* q;
+  const __bf16* k;
+  const __bf16* v;
+  __bf16* o;
+  float* lse;
+  g4_layout ql, kl, vl, ol;
+  const int* span_lo;  // per K-stream token: first position of its vision span (or itself)
+  const int* span_hi;  // per K-stream token: last position of its vision span (or itself)
+  int num_seqs;
+  int ntq;             // query tiles per sequence (set by the launcher)
+};
+
+struct BwdParams {
+  g4_problem p;
+  const __bf16* q;
+  const __bf16* k;
+  const __bf16* v;
+  const __bf16* o;
+  const __bf16* dout;
+  const float* lse;
+  const float* dlse;
+  __bf16* dq;
+  __bf16* dk;
+  __bf16* dv;
+  g4_layout ql, kl, vl, ol, dol, dql, dkl, dvl;
+  float* delta;        // (Hq, total_q) fp32 workspace, token-contiguous per head
+  const int* span_lo;
+  const int* span_hi;
+  int num_seqs;
+  int ntiles;          // row tiles per sequence (set by the launchers)
+};
+
+// Workspace layout helpers (bytes).
+size_t spans_bytes(const g4_problem& p);
+size_t delta_bytes(const g4_problem& p);
+int64_t k_stream_tokens(const g4_problem& p);
+int64_t q_stream_tokens(const g4_problem& p);
+
+hipError_t launch_spans(const g4_problem& p, void* ws, hipStream_t stream);
+void span_arrays(const g4_problem& p, void* ws, const int** lo, const int** hi);
+hipError_t launch_fwd(const FwdParams& a, hipStream_t stream);
+hipError_t launch_bwd_delta(const BwdParams& a, hipStream_t stream);
+hipError_t launch_bwd_dkdv(const BwdParams& a, hipStream_t stream);
+hipError_t launch_bwd_dq(const BwdParams& a, hipStream_t stream);
+hipError_t launch_mask(const g4_problem& p, uint8_t* out, const int* span_lo, const int* span_hi,
+                       hipStream_t stream);
+hipError_t launch_ranges(const g4_problem& p, int direction, int row_tile, int32_t* out,
+                         const int* span_lo, const int* span_hi, hipStream_t stream);
+
+}  // namespace g4

@@ -1,0 +1,244 @@
+// Mask metadata kernels: vision spans, mask materialisation, scheduler ranges.
+//
+// Vision span of a K-stream token t with vision ID >= 0: the first and last
+// position, within t's sequence, of the tokens sharing t's (document, vision)
+// pair.  For the local Gemma mask a query at position a may attend future keys
+// only inside its span (no right window cap), and a key at position j may be
+// attended by earlier queries only inside its span, so the spans bound the
+// key range of a query tile and the query range of a key tile exactly, for
+// any ID pattern (repeated or non-contiguous IDs included).  They are computed
+// on device with one open-addressing hash table per sequence (2 * Lk slots),
+// O(tokens), no host round trip.
+#include "g4_kernels.h"
+
+namespace g4 {
+
+namespace {
+
+constexpr unsigned long long kEmpty = ~0ull;
+
+struct SpanWs {
+  int* lo;
+  int* hi;
+  unsigned long long* keys;
+  int* first;
+  int* last;
+};
+
+__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+__host__ __device__ inline SpanWs span_ws(void* ws, int64_t tk) {
+  char* b = (char*)ws;
+  SpanWs w;
+  w.lo = (int*)b;
+  b += align256(tk * 4);
+  w.hi = (int*)b;
+  b += align256(tk * 4);
+  w.keys = (unsigned long long*)b;
+  b += align256(2 * tk * 8);
+  w.first = (int*)b;
+  b += align256(2 * tk * 4);
+  w.last = (int*)b;
+  return w;
+}
+
+// Sequence holding K-stream token t, with its start and length.
+__device__ inline void seq_of_token(const g4_problem& p, int64_t t, int& s, int64_t& ks, int& lk) {
+  if (p.cu_seqlens_k == nullptr) {
+    s = (int)(t / p.seqlen_k);
+    ks = (int64_t)s * p.seqlen_k;
+    lk = p.seqlen_k;
+    return;
+  }
+  int lo = 0, hi = p.num_seqs;  // find last s with cu[s] <= t
+  while (hi - lo > 1) {
+    int mid = (lo + hi) >> 1;
+    if (p.cu_seqlens_k[mid] <= t) lo = mid; else hi = mid;
+  }
+  s = lo;
+  ks = p.cu_seqlens_k[lo];
+  lk = p.cu_seqlens_k[lo + 1] - p.cu_seqlens_k[lo];
+}
+
+__device__ inline unsigned long long span_key(const g4_problem& p, int64_t t, int vid) {
+  unsigned doc = p.document_ids ? (unsigned)p.document_ids[t] : 0u;
+  return ((unsigned long long)doc << 32) | (unsigned)vid;
+}
+
+__device__ inline int64_t probe_slot(SpanWs w, int64_t base, int64_t cap, unsigned long long key,
+                                     bool insert) {
+  unsigned long long h = key * 0x9E3779B97F4A7C15ull;
+  int64_t slot = (int64_t)((h >> 32) % (unsigned long long)cap);
+  for (int64_t n = 0; n < cap; ++n) {
+    unsigned long long* cell = w.keys + base + slot;
+    unsigned long long cur = insert ? atomicCAS(cell, kEmpty, key) : *cell;
+    if (cur == key || (insert && cur == kEmpty)) return base + slot;
+    slot = slot + 1 == cap ? 0 : slot + 1;
+  }
+  return -1;  // unreachable: the table holds at most Lk keys in 2 * Lk slots
+}
+
+__global__ void span_init_kernel(SpanWs w, int64_t nslots) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nslots;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    w.keys[i] = kEmpty;
+    w.first[i] = 0x7fffffff;
+    w.last[i] = -1;
+  }
+}
+
+__global__ void span_insert_kernel(g4_problem p, SpanWs w, int64_t tk) {
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < tk;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    int vid = p.vision_ids[t];
+    if (vid < 0) continue;
+    int s, lk;
+    int64_t ks;
+    seq_of_token(p, t, s, ks, lk);
+    int64_t slot = probe_slot(w, 2 * ks, 2 * (int64_t)lk, span_key(p, t, vid), true);
+    if (slot < 0) continue;
+    int j = (int)(t - ks);
+    atomicMin(w.first + slot, j);
+    atomicMax(w.last + slot, j);
+  }
+}
+
+__global__ void span_lookup_kernel(g4_problem p, SpanWs w, int64_t tk) {
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < tk;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    int s, lk;
+    int64_t ks;
+    seq_of_token(p, t, s, ks, lk);
+    int j = (int)(t - ks);
+    int vid = p.vision_ids[t];
+    int lo = j, hi = j;
+    if (vid >= 0) {
+      int64_t slot = probe_slot(w, 2 * ks, 2 * (int64_t)lk, span_key(p, t, vid), false);
+      if (slot >= 0) {
+        lo = w.first[slot];
+        hi = w.last[slot];
+      }
+    }
+    w.lo[t] = lo;
+    w.hi[t] = hi;
+  }
+}
+
+__global__ void mask_kernel(g4_problem p, uint8_t* out) {
+  const int64_t per_seq = (int64_t)p.seqlen_q * p.seqlen_k;
+  const int64_t n = per_seq * p.num_seqs;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    int s = (int)(e / per_seq);
+    int64_t r = e % per_seq;
+    int i = (int)(r / p.seqlen_k), j = (int)(r % p.seqlen_k);
+    Seq sq = resolve_seq(p, s);
+    uint8_t v = 0;
+    if (i < sq.lq && j < sq.lk) {
+      int a = i + sq.lk - sq.lq;
+      bool has_vid = p.vision_ids != nullptr && p.bidirectional_vision;
+      bool has_doc = p.document_ids != nullptr;
+      int vq = has_vid ? p.vision_ids[sq.ktok + a] : -1;
+      int vk = has_vid ? p.vision_ids[sq.ktok + j] : -1;
+      int dq = has_doc ? p.document_ids[sq.ktok + a] : 0;
+      int dk = has_doc ? p.document_ids[sq.ktok + j] : 0;
+      v = allowed(a, j, p.window, has_vid, vq, vk, has_doc, dq, dk) ? 1 : 0;
+    }
+    out[e] = v;
+  }
+}
+
+__global__ void ranges_kernel(g4_problem p, int direction, int row_tile, int ntiles, int32_t* out,
+                              const int* span_lo, const int* span_hi) {
+  int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= p.num_seqs * ntiles) return;
+  int s = e / ntiles, t = e % ntiles;
+  Seq sq = resolve_seq(p, s);
+  int off = sq.lk - sq.lq;
+  bool has_vid = p.vision_ids != nullptr && p.bidirectional_vision;
+  int lo = 0, hi = 0;
+  if (direction == 0) {
+    int i0 = t * row_tile;
+    if (i0 < sq.lq) {
+      int i1 = min(i0 + row_tile, sq.lq) - 1;
+      int smax = -1;
+      if (has_vid)
+        for (int i = i0; i <= i1; ++i) smax = max(smax, span_hi[sq.ktok + i + off]);
+      query_tile_key_range(i0 + off, i1 + off, sq.lk, p.window, smax, lo, hi);
+    }
+  } else {
+    int j0 = t * row_tile;
+    if (j0 < sq.lk) {
+      int j1 = min(j0 + row_tile, sq.lk) - 1;
+      int smin = 0x7fffffff;
+      if (has_vid)
+        for (int j = j0; j <= j1; ++j) smin = min(smin, span_lo[sq.ktok + j]);
+      key_tile_query_range(j0, j1, sq.lq, off, p.window, smin, lo, hi);
+    }
+  }
+  out[2 * e] = lo;
+  out[2 * e + 1] = hi;
+}
+
+int grid_for(int64_t n, int block) {
+  int64_t g = (n + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > 65536) g = 65536;
+  return (int)g;
+}
+
+}  // namespace
+
+int64_t k_stream_tokens(const g4_problem& p) {
+  return p.cu_seqlens_k ? p.total_k : (int64_t)p.num_seqs * p.seqlen_k;
+}
+
+int64_t q_stream_tokens(const g4_problem& p) {
+  return p.cu_seqlens_q ? p.total_q : (int64_t)p.num_seqs * p.seqlen_q;
+}
+
+size_t spans_bytes(const g4_problem& p) {
+  if (p.vision_ids == nullptr || !p.bidirectional_vision) return 0;
+  int64_t tk = k_stream_tokens(p);
+  return align256(tk * 4) * 2 + align256(2 * tk * 8) + align256(2 * tk * 4) * 2;
+}
+
+hipError_t launch_spans(const g4_problem& p, void* ws, hipStream_t stream) {
+  int64_t tk = k_stream_tokens(p);
+  SpanWs w = span_ws(ws, tk);
+  span_init_kernel<<<grid_for(2 * tk, 256), 256, 0, stream>>>(w, 2 * tk);
+  span_insert_kernel<<<grid_for(tk, 256), 256, 0, stream>>>(p, w, tk);
+  span_lookup_kernel<<<grid_for(tk, 256), 256, 0, stream>>>(p, w, tk);
+  return hipGetLastError();
+}
+
+hipError_t launch_mask(const g4_problem& p, uint8_t* out, const int*, const int*,
+                       hipStream_t stream) {
+  int64_t n = (int64_t)p.seqlen_q * p.seqlen_k * p.num_seqs;
+  mask_kernel<<<grid_for(n, 256), 256, 0, stream>>>(p, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_ranges(const g4_problem& p, int direction, int row_tile, int32_t* out,
+                         const int* span_lo, const int* span_hi, hipStream_t stream) {
+  int len = direction == 0 ? p.seqlen_q : p.seqlen_k;
+  int ntiles = (len + row_tile - 1) / row_tile;
+  int n = ntiles * p.num_seqs;
+  if (n <= 0) return hipSuccess;
+  ranges_kernel<<<(n + 127) / 128, 128, 0, stream>>>(p, direction, row_tile, ntiles, out, span_lo,
+                                                     span_hi);
+  return hipGetLastError();
+}
+
+// Span arrays inside a workspace produced by launch_spans.
+void span_arrays(const g4_problem& p, void* ws, const int** lo, const int** hi) {
+  if (spans_bytes(p) == 0) {
+    *lo = *hi = nullptr;
+    return;
+  }
+  SpanWs w = span_ws(ws, k_stream_tokens(p));
+  *lo = w.lo;
+  *hi = w.hi;
+}
+
+}  // namespace g4

@@ -1,0 +1,703 @@
+"""Drop-in MI355X adapters for the Gemma 4 attention hot path.
+
+Same public functions, keyword arguments, return contracts, validation and
+error classes as the reference adapters in ``src/gemma4_fa4/h100.py``
+(750-1394); underneath, every call launches the hand-written gfx950 kernels of
+``libgemma4_attn.so`` on the caller's current stream:
+
+* forward: one launch for the full head dimension (no V slabs, no LSE
+  equality sync) plus, with vision IDs, the O(T) device span table;
+* backward: delta pre-pass, dK/dV (KV-tile major, GQA group reduced on chip,
+  distinct dK and dV) and dQ (Q-tile major); no atomics, so gradients repeat
+  bitwise.
+
+Fixed inputs are BSHD ``(B, S, H, D)``; packed inputs are THD ``(T, H, D)``
+with int32 ``cu_seqlens``; LSE is fp32 ``(B, Hq, S)`` or ``(Hq, Tq)`` and is
+differentiable.  Queries are the lower-right suffix of their key sequence.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import G4Layout, G4Problem
+from .errors import GlobalBackwardBudgetExceeded, UnsupportedMI355XPath
+from .model_spec import GEMMA4_31B, GLOBAL_ATTENTION, SLIDING_ATTENTION, AttentionLayerSpec
+
+_LOCAL_CUSTOM_DENSE_MAX_SEQLEN = 1025
+_LOCAL_MODEL_MAX_SEQLEN = GEMMA4_31B.max_position_embeddings
+_GLOBAL_FIXED_BACKWARD_MAX_SEQLEN = 2048
+_GLOBAL_NATIVE_BACKWARD_MAX_SEQLEN = _LOCAL_MODEL_MAX_SEQLEN
+_GLOBAL_BACKWARD_RESERVE_BYTES = 2 * 1024**3
+_METADATA_WORKSPACE_MAX_BYTES = 2 * 1024**3
+_TARGET_ARCH = "gfx950"
+
+
+# ---------------------------------------------------------------------------
+# validation (mirrors h100.py:131-367, 604-684, 1039-1145)
+# ---------------------------------------------------------------------------
+
+
+def _is_fake_tensor(tensor: torch.Tensor) -> bool:
+    try:
+        from torch._subclasses.fake_tensor import FakeTensor
+    except ImportError:  # pragma: no cover
+        return False
+    return isinstance(tensor, FakeTensor)
+
+
+def _require_gfx950(device: torch.device) -> None:
+    if device.type != "cuda":
+        raise UnsupportedMI355XPath("MI355X attention inputs must be GPU tensors")
+    arch = torch.cuda.get_device_properties(device).gcnArchName
+    if not arch.startswith(_TARGET_ARCH):
+        raise UnsupportedMI355XPath(f"MI355X attention requires {_TARGET_ARCH}, found {arch}")
+
+
+def _has_proven_nonoverlap(tensor: torch.Tensor) -> bool:
+    """Prove a positive-stride layout non-overlapping (mixed-radix argument)."""
+    overlap = torch._debug_has_internal_overlap(tensor)
+    if overlap == 0:
+        return True
+    if overlap == 1:
+        return False
+    covered = 0
+    for stride, size in sorted(
+        (st, sz) for sz, st in zip(tensor.shape, tensor.stride()) if sz > 1
+    ):
+        if stride <= covered:
+            return False
+        covered += (size - 1) * stride
+    return True
+
+
+def _validate_layout(tensor: torch.Tensor, *, name: str) -> None:
+    if tensor.stride(-1) != 1:
+        raise ValueError(f"{name} must have unit last-dimension stride")
+    if any(stride <= 0 for stride in tensor.stride()):
+        raise ValueError(f"{name} must use positive, non-broadcast strides")
+    if any(stride % 8 for stride in tensor.stride()[:-1]):
+        raise ValueError(f"{name} outer strides must be 16-byte aligned for BF16")
+    if not _has_proven_nonoverlap(tensor):
+        raise ValueError(f"{name} must use a non-overlapping layout")
+
+
+def _check_real_operands(tensors, names, *, label: str) -> None:
+    fake = [_is_fake_tensor(t) for t in tensors]
+    if any(fake):
+        raise UnsupportedMI355XPath(f"{label}: fake tensors are not supported by the MI355X path")
+    if any(t.data_ptr() % 16 for t in tensors):
+        raise ValueError(f"{label} base pointers must be 16-byte aligned")
+
+
+def _validate_bshd(q, k, v, spec: AttentionLayerSpec, *, require_device: bool = True) -> None:
+    if any(t.ndim != 4 for t in (q, k, v)):
+        raise ValueError("q, k, and v must be rank-4 B/S/H/D tensors")
+    if not (q.device == k.device == v.device):
+        raise ValueError("q, k, and v must be on one device")
+    if any(t.dtype != torch.bfloat16 for t in (q, k, v)):
+        raise ValueError("the MI355X path accepts BF16 q, k, and v only")
+    for name, tensor in zip(("q", "k", "v"), (q, k, v)):
+        _validate_layout(tensor, name=name)
+    _check_real_operands((q, k, v), ("q", "k", "v"), label="q, k, and v")
+    batch, seqlen, q_heads, q_dim = q.shape
+    if batch <= 0 or seqlen <= 0:
+        raise ValueError("batch and sequence length must be positive")
+    if (q_heads, q_dim) != (spec.num_q_heads, spec.head_dim_qk):
+        raise ValueError("q shape does not match the attention spec")
+    if k.shape != (batch, seqlen, spec.num_kv_heads, spec.head_dim_qk) or v.shape != (
+        batch,
+        seqlen,
+        spec.num_kv_heads,
+        spec.head_dim_v,
+    ):
+        raise ValueError("k/v shapes do not match the attention spec")
+    if spec.qhead_per_kvhead not in {1, 2, 4, 8}:
+        raise ValueError("the validated GQA ratios are 1, 2, 4, and 8")
+    if k.untyped_storage().data_ptr() == v.untyped_storage().data_ptr():
+        raise ValueError("K and V must be distinct, non-aliasing prepared operands")
+    if require_device:
+        _require_gfx950(q.device)
+
+
+def _locked_local(spec: AttentionLayerSpec, *, check_kv_heads: bool) -> bool:
+    return (
+        spec.kind == "sliding_attention"
+        and spec.head_dim_qk == 256
+        and spec.head_dim_v == 256
+        and spec.num_q_heads == 32
+        and (not check_kv_heads or spec.num_kv_heads == 16)
+        and spec.softmax_scale == 1.0
+        and spec.sliding_window == 1024
+        and spec.is_causal
+    )
+
+
+def _locked_global(spec: AttentionLayerSpec) -> bool:
+    return (
+        spec.kind == "full_attention"
+        and spec.head_dim_qk == 512
+        and spec.head_dim_v == 512
+        and spec.num_q_heads == 32
+        and spec.num_kv_heads == 4
+        and spec.softmax_scale == 1.0
+        and spec.sliding_window is None
+        and spec.is_causal
+    )
+
+
+def _validate_local_bshd(q, k, v, spec, *, require_device: bool = True) -> None:
+    _validate_bshd(q, k, v, spec, require_device=require_device)
+    if q.shape[0] != 1 or q.shape[1] > _LOCAL_CUSTOM_DENSE_MAX_SEQLEN:
+        raise UnsupportedMI355XPath("fixed local attention covers only B=1 and 1 <= S <= 1025")
+    if not _locked_local(spec, check_kv_heads=False):
+        raise UnsupportedMI355XPath("only the locked local d256 attention contract is enabled")
+
+
+def _normalize_int32_metadata(values: torch.Tensor, *, name: str) -> torch.Tensor:
+    if values.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"{name} must use INT32 or INT64 values")
+    if values.requires_grad:
+        raise ValueError(f"{name} must not require gradients")
+    if values.dtype == torch.int64 and values.numel():
+        lo, hi = torch.aminmax(values)
+        info = torch.iinfo(torch.int32)
+        if lo.item() < info.min or hi.item() > info.max:
+            raise ValueError(f"INT64 {name} values must fit exactly in INT32")
+    return values.to(dtype=torch.int32).contiguous()
+
+
+def _prepare_vision_block_ids(vision_block_ids: torch.Tensor, q: torch.Tensor) -> torch.Tensor:
+    expected = q.shape[:2]
+    if vision_block_ids.shape != expected:
+        raise ValueError(
+            f"vision_block_ids must have shape {expected}, got {tuple(vision_block_ids.shape)}"
+        )
+    if vision_block_ids.device != q.device:
+        raise ValueError("vision_block_ids must be on the same device as q, k, and v")
+    return _normalize_int32_metadata(vision_block_ids, name="vision_block_ids").view(-1)
+
+
+def _cumulative_lengths(cu_q, cu_k, q, k, *, label: str):
+    q_vals = [int(x) for x in cu_q.detach().cpu().tolist()]
+    k_vals = [int(x) for x in cu_k.detach().cpu().tolist()]
+    if q_vals[0] != 0 or k_vals[0] != 0:
+        raise ValueError(f"{label} cumulative arrays must start at zero")
+    if q_vals[-1] != q.shape[0] or k_vals[-1] != k.shape[0]:
+        raise ValueError(f"{label} cumulative arrays must end at the packed Q/K totals")
+    q_lengths = [e - s for s, e in zip(q_vals[:-1], q_vals[1:])]
+    k_lengths = [e - s for s, e in zip(k_vals[:-1], k_vals[1:])]
+    if any(length < 0 for length in (*q_lengths, *k_lengths)):
+        raise ValueError(f"{label} cumulative arrays must be nondecreasing")
+    return q_lengths, k_lengths
+
+
+def _validate_packed_common(q, k, v, cu_q, cu_k, max_q, max_k, *, label: str):
+    if any(t.ndim != 3 for t in (q, k, v)):
+        raise ValueError(f"{label} q, k, and v must be rank-3 T/H/D tensors")
+    if not (q.device == k.device == v.device):
+        raise ValueError(f"{label} q, k, and v must be on one device")
+    if any(t.dtype != torch.bfloat16 for t in (q, k, v)):
+        raise ValueError(f"{label} q, k, and v must use BF16")
+    if q.shape[0] <= 0 or k.shape[0] <= 0:
+        raise ValueError(f"{label} Q and K totals must be positive")
+    for name, tensor in zip(("packed q", "packed k", "packed v"), (q, k, v)):
+        _validate_layout(tensor, name=name)
+    _check_real_operands((q, k, v), ("q", "k", "v"), label=f"{label} q, k, and v")
+    if k.untyped_storage().data_ptr() == v.untyped_storage().data_ptr():
+        raise ValueError("K and V must be distinct, non-aliasing prepared operands")
+    if any(isinstance(x, bool) or not isinstance(x, int) for x in (max_q, max_k)):
+        raise TypeError("max_seqlen_q and max_seqlen_k must be Python integers")
+    cumulative = (cu_q, cu_k)
+    if any(t.ndim != 1 or t.numel() < 2 for t in cumulative):
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must be rank-1 B+1 tensors")
+    if cu_q.shape != cu_k.shape:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must have the same batch count")
+    if any(t.device != q.device for t in cumulative):
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must share the q/k/v device")
+    if any(t.dtype != torch.int32 for t in cumulative):
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must use INT32")
+    if any(not t.is_contiguous() for t in cumulative):
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must be contiguous")
+
+
+def _validate_local_varlen(q, k, v, cu_q, cu_k, max_q, max_k, spec, *, require_device=True):
+    _validate_packed_common(q, k, v, cu_q, cu_k, max_q, max_k, label="packed")
+    if q.shape[1:] != (spec.num_q_heads, spec.head_dim_qk):
+        raise ValueError("packed q shape does not match the attention spec")
+    if k.shape[1:] != (spec.num_kv_heads, spec.head_dim_qk):
+        raise ValueError("packed k shape does not match the attention spec")
+    if v.shape != (k.shape[0], spec.num_kv_heads, spec.head_dim_v):
+        raise ValueError("packed v shape does not match the attention spec")
+    if not _locked_local(spec, check_kv_heads=True):
+        raise UnsupportedMI355XPath("only the locked local d256 GQA-2 varlen contract is enabled")
+    if max_q <= 0 or max_k <= 0 or max_k > _LOCAL_MODEL_MAX_SEQLEN:
+        raise UnsupportedMI355XPath("varlen local attention requires 1 <= max Sq <= max Sk <= 262144")
+    if max_q > max_k:
+        raise UnsupportedMI355XPath("varlen local attention requires max Sq <= max Sk")
+    q_lengths, k_lengths = _cumulative_lengths(cu_q, cu_k, q, k, label="packed")
+    if any(lq > lk for lq, lk in zip(q_lengths, k_lengths)):
+        raise UnsupportedMI355XPath("each packed sequence requires Sq <= Sk")
+    if max(q_lengths) != max_q or max(k_lengths) != max_k:
+        raise ValueError("max_seqlen_q/max_seqlen_k must equal the cumulative maxima")
+    if require_device:
+        _require_gfx950(q.device)
+    return q_lengths, k_lengths
+
+
+def _prepare_packed_k_metadata(values, k: torch.Tensor, *, name: str):
+    if values is None:
+        return None
+    if values.shape != (k.shape[0],):
+        raise ValueError(f"{name} must have shape ({k.shape[0]},)")
+    if values.device != k.device:
+        raise ValueError(f"{name} must share the q/k/v device")
+    return _normalize_int32_metadata(values, name=name)
+
+
+def _validate_global_bshd(q, k, v, spec, *, require_device: bool = True) -> None:
+    _validate_bshd(q, k, v, spec, require_device=require_device)
+    if q.shape[0] != 1 or q.shape[1] > _GLOBAL_FIXED_BACKWARD_MAX_SEQLEN:
+        raise UnsupportedMI355XPath("fixed global backward requires B=1 and 1 <= S <= 2048")
+    if not _locked_global(spec):
+        raise UnsupportedMI355XPath("only the locked global d512 text-forward contract is enabled")
+
+
+def _validate_global_forward_only_bshd(q, k, v, spec) -> None:
+    if any(t.ndim != 4 for t in (q, k, v)):
+        raise ValueError("global forward-only q, k, and v must be rank-4 B/S/H/D tensors")
+    if not (q.device == k.device == v.device):
+        raise ValueError("global forward-only q, k, and v must be on one device")
+    if any(t.dtype != torch.bfloat16 for t in (q, k, v)):
+        raise ValueError("global forward-only q, k, and v must use BF16")
+    for name, tensor in zip(("q", "k", "v"), (q, k, v)):
+        _validate_layout(tensor, name=name)
+    _check_real_operands((q, k, v), ("q", "k", "v"), label="global forward-only q, k, and v")
+    if k.untyped_storage().data_ptr() == v.untyped_storage().data_ptr():
+        raise ValueError("global forward-only K and V must be distinct operands")
+    batch, q_len, q_heads, q_dim = q.shape
+    kv_len = k.shape[1]
+    if batch <= 0 or not (1 <= q_len <= kv_len <= _LOCAL_MODEL_MAX_SEQLEN):
+        raise UnsupportedMI355XPath("global forward-only requires B>=1 and 1 <= Sq <= Sk <= 262144")
+    if (q_heads, q_dim) != (spec.num_q_heads, spec.head_dim_qk):
+        raise ValueError("global forward-only q shape conflicts with the locked geometry")
+    if k.shape != (batch, kv_len, spec.num_kv_heads, spec.head_dim_qk):
+        raise ValueError("global forward-only k shape conflicts with the locked geometry")
+    if v.shape != (batch, kv_len, spec.num_kv_heads, spec.head_dim_v):
+        raise ValueError("global forward-only v shape conflicts with the locked geometry")
+    if not _locked_global(spec):
+        raise UnsupportedMI355XPath("only the locked global d512 contract is enabled")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        raise UnsupportedMI355XPath(
+            "global forward-only cannot participate in autograd; use "
+            "fa4_global_text_forward for S<=2048 or packed fa4_global_varlen_forward"
+        )
+    _require_gfx950(q.device)
+
+
+def _validate_global_varlen(q, k, v, cu_q, cu_k, max_q, max_k, spec, *, allow_backward=False):
+    _validate_packed_common(q, k, v, cu_q, cu_k, max_q, max_k, label="global packed")
+    if q.shape[1:] != (spec.num_q_heads, spec.head_dim_qk):
+        raise ValueError("global packed q shape conflicts with the lock")
+    if k.shape[1:] != (spec.num_kv_heads, spec.head_dim_qk):
+        raise ValueError("global packed k shape conflicts with the lock")
+    if v.shape != (k.shape[0], spec.num_kv_heads, spec.head_dim_v):
+        raise ValueError("global packed v shape conflicts with the lock")
+    if not _locked_global(spec):
+        raise UnsupportedMI355XPath("only the locked global d512 contract is enabled")
+    max_supported = _GLOBAL_NATIVE_BACKWARD_MAX_SEQLEN if allow_backward else _LOCAL_MODEL_MAX_SEQLEN
+    if not (1 <= max_q <= max_k <= max_supported):
+        op = "backward-capable" if allow_backward else "forward-only"
+        raise UnsupportedMI355XPath(
+            f"global packed {op} maxima must satisfy 1 <= Sq <= Sk <= {max_supported}"
+        )
+    if not allow_backward and torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        raise UnsupportedMI355XPath(
+            "global packed forward-only cannot participate in autograd; use "
+            "fa4_global_varlen_forward"
+        )
+    q_lengths, k_lengths = _cumulative_lengths(cu_q, cu_k, q, k, label="global packed")
+    if any(lq > lk for lq, lk in zip(q_lengths, k_lengths)):
+        raise UnsupportedMI355XPath("global packed segments require 0 <= Sq <= Sk per segment")
+    if max(q_lengths) != max_q or max(k_lengths) != max_k:
+        raise ValueError("global packed maxima must equal the cumulative segment maxima")
+    if q.shape[0] > torch.iinfo(torch.int32).max or k.shape[0] > torch.iinfo(torch.int32).max:
+        raise UnsupportedMI355XPath("packed global totals must fit signed INT32")
+    _require_gfx950(q.device)
+    return q_lengths, k_lengths
+
+
+# ---------------------------------------------------------------------------
+# launch plan
+# ---------------------------------------------------------------------------
+
+
+def _layout(t: torch.Tensor, packed: bool) -> G4Layout:
+    if packed:
+        return G4Layout(0, t.stride(0), t.stride(1))
+    return G4Layout(t.stride(0), t.stride(1), t.stride(2))
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+@dataclass
+class _Plan:
+    """Geometry of one attention call, shared by its forward and backward."""
+
+    packed: bool
+    num_seqs: int
+    seqlen_q: int  # fixed length, or maximum when packed
+    seqlen_k: int
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    window: int
+    bidirectional: bool
+    total_q: int
+    total_k: int
+    cu_q: torch.Tensor | None = None
+    cu_k: torch.Tensor | None = None
+    vision: torch.Tensor | None = None
+    documents: torch.Tensor | None = None
+
+    def problem(self) -> G4Problem:
+        p = G4Problem()
+        p.num_seqs = self.num_seqs
+        p.seqlen_q = self.seqlen_q
+        p.seqlen_k = self.seqlen_k
+        p.num_q_heads = self.num_q_heads
+        p.num_kv_heads = self.num_kv_heads
+        p.head_dim = self.head_dim
+        p.window = self.window
+        p.bidirectional_vision = 1 if self.bidirectional else 0
+        p.total_q = self.total_q
+        p.total_k = self.total_k
+        p.cu_seqlens_q = _ptr(self.cu_q)
+        p.cu_seqlens_k = _ptr(self.cu_k)
+        p.vision_ids = _ptr(self.vision)
+        p.document_ids = _ptr(self.documents)
+        if self.packed:
+            p.lse_batch_stride = 0
+            p.lse_head_stride = self.total_q
+        else:
+            p.lse_batch_stride = self.num_q_heads * self.seqlen_q
+            p.lse_head_stride = self.seqlen_q
+        return p
+
+    def lse_shape(self) -> tuple[int, ...]:
+        if self.packed:
+            return (self.num_q_heads, self.total_q)
+        return (self.num_seqs, self.num_q_heads, self.seqlen_q)
+
+    def workspace_bytes(self, phase: int) -> int:
+        lib = _lib.load()
+        prob = self.problem()
+        nbytes = lib.g4_workspace_bytes(ctypes.byref(prob), phase)
+        if nbytes == 0 and lib.g4_last_error():
+            _lib.check(_lib.G4_ERR_INVALID)
+        return int(nbytes)
+
+    def _workspace(self, phase: int, device) -> torch.Tensor:
+        return torch.empty(max(self.workspace_bytes(phase), 256), dtype=torch.uint8, device=device)
+
+    def forward(self, q, k, v):
+        lib = _lib.load()
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        lse = torch.empty(self.lse_shape(), dtype=torch.float32, device=q.device)
+        ws = self._workspace(0, q.device)
+        prob = self.problem()
+        with torch.cuda.device(q.device):
+            stream = torch.cuda.current_stream(q.device).cuda_stream
+            rc = lib.g4_attn_fwd(
+                ctypes.byref(prob),
+                q.data_ptr(), _layout(q, self.packed),
+                k.data_ptr(), _layout(k, self.packed),
+                v.data_ptr(), _layout(v, self.packed),
+                out.data_ptr(), _layout(out, self.packed),
+                lse.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+            )
+        _lib.check(rc)
+        return out, lse
+
+    def backward(self, q, k, v, out, dout, lse, dlse):
+        lib = _lib.load()
+        if dout.stride(-1) != 1 or any(s % 8 for s in dout.stride()[:-1]):
+            dout = dout.contiguous()
+        if dlse is not None:
+            dlse = dlse.to(torch.float32).contiguous()
+        dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+        dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+        ws = self._workspace(1, q.device)
+        prob = self.problem()
+        with torch.cuda.device(q.device):
+            stream = torch.cuda.current_stream(q.device).cuda_stream
+            rc = lib.g4_attn_bwd(
+                ctypes.byref(prob),
+                q.data_ptr(), _layout(q, self.packed),
+                k.data_ptr(), _layout(k, self.packed),
+                v.data_ptr(), _layout(v, self.packed),
+                out.data_ptr(), _layout(out, self.packed),
+                dout.data_ptr(), _layout(dout, self.packed),
+                lse.data_ptr(), _ptr(dlse),
+                dq.data_ptr(), _layout(dq, self.packed),
+                dk.data_ptr(), _layout(dk, self.packed),
+                dv.data_ptr(), _layout(dv, self.packed),
+                ws.data_ptr(), ws.numel(), stream,
+            )
+        _lib.check(rc)
+        return dq, dk, dv
+
+
+class _AttentionFunction(torch.autograd.Function):
+    """Forward saves (q, k, v, O, LSE); backward accepts dO and dLSE (either may be None)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, plan: _Plan):
+        out, lse = plan.forward(q, k, v)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.plan = plan
+        ctx.set_materialize_grads(False)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        q, k, v, out, lse = ctx.saved_tensors
+        if dout is None:
+            dout = torch.zeros_like(out)
+        dq, dk, dv = ctx.plan.backward(q, k, v, out, dout, lse, dlse)
+        return dq, dk, dv, None
+
+
+def _fixed_plan(q, k, spec: AttentionLayerSpec, *, vision=None) -> _Plan:
+    b, sq, hq, d = q.shape
+    return _Plan(
+        packed=False,
+        num_seqs=b,
+        seqlen_q=sq,
+        seqlen_k=k.shape[1],
+        num_q_heads=hq,
+        num_kv_heads=k.shape[2],
+        head_dim=d,
+        window=spec.sliding_window or 0,
+        bidirectional=bool(spec.vision_bidirectional_within_block and vision is not None),
+        total_q=b * sq,
+        total_k=b * k.shape[1],
+        vision=vision,
+    )
+
+
+def _packed_plan(q, k, cu_q, cu_k, max_q, max_k, spec, *, vision=None, documents=None) -> _Plan:
+    return _Plan(
+        packed=True,
+        num_seqs=cu_q.numel() - 1,
+        seqlen_q=max_q,
+        seqlen_k=max_k,
+        num_q_heads=q.shape[1],
+        num_kv_heads=k.shape[1],
+        head_dim=q.shape[2],
+        window=spec.sliding_window or 0,
+        bidirectional=bool(spec.vision_bidirectional_within_block and vision is not None),
+        total_q=q.shape[0],
+        total_k=k.shape[0],
+        cu_q=cu_q,
+        cu_k=cu_k,
+        vision=vision,
+        documents=documents,
+    )
+
+
+# ---------------------------------------------------------------------------
+# HBM preflights (fail closed before any launch; policy of h100.py:425-442, 713-746)
+# ---------------------------------------------------------------------------
+
+
+def _free_hbm(device) -> int:
+    free, _total = torch.cuda.mem_get_info(device)
+    return free
+
+
+def _preflight_metadata_workspace(plan: _Plan, device) -> None:
+    required = plan.workspace_bytes(1)
+    if required > _METADATA_WORKSPACE_MAX_BYTES:
+        raise UnsupportedMI355XPath(
+            f"vision-span workspace requires {required} bytes, above the 2 GiB safety limit"
+        )
+    free = _free_hbm(device)
+    if required > free // 10:
+        raise UnsupportedMI355XPath(
+            f"vision-span workspace requires {required} bytes, exceeding the 10% free-HBM "
+            f"budget of {free // 10} bytes ({free} bytes free)"
+        )
+
+
+def _global_backward_budget(free_bytes: int) -> int:
+    return min(free_bytes * 4 // 5, max(0, free_bytes - _GLOBAL_BACKWARD_RESERVE_BYTES))
+
+
+def _check_global_backward_budget(required: int, free: int) -> None:
+    budget = _global_backward_budget(free)
+    if required > budget:
+        raise GlobalBackwardBudgetExceeded(
+            f"global backward needs about {required} additional bytes, above the guarded "
+            f"budget of {budget} bytes ({free} bytes currently free)"
+        )
+
+
+def _backward_additional_bytes(plan: _Plan, q, k, v) -> int:
+    grads = sum(t.numel() * t.element_size() for t in (q, k, v))
+    return grads + plan.workspace_bytes(1)
+
+
+def _preflight_backward(plan: _Plan, q, k, v) -> None:
+    _check_global_backward_budget(_backward_additional_bytes(plan, q, k, v), _free_hbm(q.device))
+
+
+def _preflight_forward_outputs(q: torch.Tensor) -> None:
+    out_bytes = q.numel() * q.element_size()
+    lse_bytes = q.numel() // q.shape[-1] * 4
+    required = 2 * (out_bytes + lse_bytes)
+    free = _free_hbm(q.device)
+    if required > free * 8 // 10:
+        raise UnsupportedMI355XPath(
+            f"forward outputs require about {required} bytes, above 80% of the {free} "
+            "currently free HBM bytes"
+        )
+
+
+def _requires_backward(*tensors) -> bool:
+    return torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
+
+
+def _run(q, k, v, plan: _Plan):
+    if _requires_backward(q, k, v):
+        return _AttentionFunction.apply(q, k, v, plan)
+    return plan.forward(q, k, v)
+
+
+# ---------------------------------------------------------------------------
+# public adapters (reference names; h100.py:750-1394)
+# ---------------------------------------------------------------------------
+
+
+def fa4_local_text_forward(q, k, v, *, spec: AttentionLayerSpec = SLIDING_ATTENTION):
+    """Fixed-length local text attention (B=1, 1 <= S <= 1025), autograd-capable.
+
+    Mask ``k <= q`` and ``k > q - 1024``; LSE fp32 ``(B, Hq, S)``.
+    """
+    _validate_local_bshd(q, k, v, spec)
+    return _run(q, k, v, _fixed_plan(q, k, spec))
+
+
+def fa4_local_forward(
+    q, k, v, *, vision_block_ids=None, spec: AttentionLayerSpec = SLIDING_ATTENTION
+):
+    """Fixed-length local attention with the exact vision overlay (B=1, S <= 1025).
+
+    ``vision_block_ids=None`` is the text path.  With ``(1, S)`` IDs the mask is
+    ``(k > q - 1024) AND (k <= q OR same non-negative vision block)``.
+    """
+    if vision_block_ids is None:
+        return fa4_local_text_forward(q, k, v, spec=spec)
+    _validate_local_bshd(q, k, v, spec)
+    ids = _prepare_vision_block_ids(vision_block_ids, q)
+    plan = _fixed_plan(q, k, spec, vision=ids)
+    _preflight_metadata_workspace(plan, q.device)
+    return _run(q, k, v, plan)
+
+
+def fa4_local_varlen_forward(
+    q,
+    k,
+    v,
+    cu_seqlens_q,
+    cu_seqlens_k,
+    *,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    vision_block_ids=None,
+    document_ids=None,
+    spec: AttentionLayerSpec = SLIDING_ATTENTION,
+):
+    """Packed local attention; each Q segment is the lower-right suffix of its K segment.
+
+    Vision/document IDs follow the packed K stream.  One launch covers every
+    segment; the device scheduler bounds each tile's key range from the window
+    and the vision spans (no host schedule, no per-segment launches).
+    """
+    _validate_local_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec)
+    vision = _prepare_packed_k_metadata(vision_block_ids, k, name="vision_block_ids")
+    documents = _prepare_packed_k_metadata(document_ids, k, name="document_ids")
+    plan = _packed_plan(
+        q, k, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec,
+        vision=vision, documents=documents,
+    )
+    if vision is not None:
+        _preflight_metadata_workspace(plan, q.device)
+    return _run(q, k, v, plan)
+
+
+def fa4_global_forward_only(q, k, v, *, spec: AttentionLayerSpec = GLOBAL_ATTENTION):
+    """Fixed/rectangular global d512 forward without autograd (lower-right causal)."""
+    _validate_global_forward_only_bshd(q, k, v, spec)
+    _preflight_forward_outputs(q)
+    return _fixed_plan(q, k, spec).forward(q, k, v)
+
+
+def fa4_global_varlen_forward_only(
+    q,
+    k,
+    v,
+    cu_seqlens_q,
+    cu_seqlens_k,
+    *,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    spec: AttentionLayerSpec = GLOBAL_ATTENTION,
+):
+    """Packed lower-right global d512 forward without autograd."""
+    _validate_global_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec)
+    _preflight_forward_outputs(q)
+    plan = _packed_plan(q, k, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec)
+    return plan.forward(q, k, v)
+
+
+def fa4_global_varlen_forward(
+    q,
+    k,
+    v,
+    cu_seqlens_q,
+    cu_seqlens_k,
+    *,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    spec: AttentionLayerSpec = GLOBAL_ATTENTION,
+):
+    """Packed global d512 forward with the atomic-free MI355X backward."""
+    _validate_global_varlen(
+        q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec,
+        allow_backward=True,
+    )
+    plan = _packed_plan(q, k, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec)
+    if _requires_backward(q, k, v):
+        _preflight_backward(plan, q, k, v)
+    else:
+        _preflight_forward_outputs(q)
+    return _run(q, k, v, plan)
+
+
+def fa4_global_text_forward(q, k, v, *, spec: AttentionLayerSpec = GLOBAL_ATTENTION):
+    """Fixed-length global d512 causal attention (B=1, 1 <= S <= 2048), autograd-capable."""
+    _validate_global_bshd(q, k, v, spec)
+    plan = _fixed_plan(q, k, spec)
+    if _requires_backward(q, k, v):
+        _preflight_backward(plan, q, k, v)
+    else:
+        _preflight_forward_outputs(q)
+    return _run(q, k, v, plan)

@@ -1,0 +1,173 @@
+"""CPU tests of the drop-in boundary: library exports, validation, error classes.
+
+Mirrors the reference's fake-backend adapter tests (tests/test_h100_fa4.py:43-1300):
+every malformed input is rejected before any launch, with the reference's
+exception types and messages.
+"""
+
+import subprocess
+from dataclasses import replace
+
+import pytest
+import torch
+
+import gemma4_fa4_amd as g
+from gemma4_fa4_amd import _lib
+from gemma4_fa4_amd import attention as att
+
+
+def test_library_exports_every_declared_symbol():
+    import os
+    import re
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    header = open(os.path.join(root, "include", "gemma4_attn.h")).read()
+    declared = set(re.findall(r"^\w[\w\s\*]*?\b(g4_\w+)\(", header, flags=re.M))
+    assert declared == set(_lib.EXPORTED_SYMBOLS)
+    lib = _lib.load()
+    assert lib.g4_abi_version() == _lib.ABI_VERSION
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    for name in declared:
+        assert re.search(rf"\bT {name}$", out, flags=re.M), name
+
+
+def test_workspace_query_and_invalid_problem_are_reported():
+    import ctypes
+    lib = _lib.load()
+    p = _lib.G4Problem(num_seqs=1, seqlen_q=128, seqlen_k=128, num_q_heads=32, num_kv_heads=16,
+                       head_dim=256, window=1024)
+    assert lib.g4_workspace_bytes(ctypes.byref(p), 0) == 0  # no vision: no span table
+    assert lib.g4_workspace_bytes(ctypes.byref(p), 1) >= 32 * 128 * 4
+    bad = _lib.G4Problem(num_seqs=1, seqlen_q=128, seqlen_k=128, num_q_heads=32,
+                         num_kv_heads=16, head_dim=128)
+    assert lib.g4_workspace_bytes(ctypes.byref(bad), 0) == 0
+    assert b"head_dim" in lib.g4_last_error()
+    with pytest.raises(g.UnsupportedMI355XPath, match="head_dim"):
+        _lib.check(_lib.G4_ERR_UNSUPPORTED)
+
+
+def test_error_hierarchy_keeps_reference_names():
+    assert issubclass(g.GlobalBackwardBudgetExceeded, g.UnsupportedH100Path)
+    assert g.UnsupportedH100Path is g.UnsupportedMI355XPath
+    assert issubclass(g.UnsupportedMI355XPath, RuntimeError)
+
+
+def _local(seqlen=2):
+    s = g.SLIDING_ATTENTION
+    q = torch.zeros(1, seqlen, s.num_q_heads, s.head_dim_qk, dtype=torch.bfloat16)
+    k = torch.ones(1, seqlen, s.num_kv_heads, s.head_dim_qk, dtype=torch.bfloat16)
+    v = torch.full((1, seqlen, s.num_kv_heads, s.head_dim_v), 2, dtype=torch.bfloat16)
+    return q, k, v
+
+
+def test_valid_cpu_inputs_fail_only_on_the_device_check():
+    with pytest.raises(g.UnsupportedMI355XPath, match="GPU tensors"):
+        g.fa4_local_text_forward(*_local())
+
+
+@pytest.mark.parametrize("mutate,exc,match", [
+    (lambda q, k, v: (q.float(), k, v), ValueError, "BF16"),
+    (lambda q, k, v: (q[..., :128], k, v), ValueError, "shape"),
+    (lambda q, k, v: (q, k, k), ValueError, "distinct"),
+    (lambda q, k, v: (q.transpose(-1, -2).contiguous().transpose(-1, -2), k, v), ValueError,
+     "unit last"),
+    (lambda q, k, v: (q[0], k[0], v[0]), ValueError, "rank-4"),
+])
+def test_local_fixed_rejects_malformed_inputs(mutate, exc, match):
+    with pytest.raises(exc, match=match):
+        g.fa4_local_text_forward(*mutate(*_local()))
+
+
+def test_local_fixed_envelope_is_b1_s1025(monkeypatch):
+    monkeypatch.setattr(att, "_require_gfx950", lambda _device: None)
+    with pytest.raises(g.UnsupportedMI355XPath, match="S <= 1025"):
+        g.fa4_local_text_forward(*_local(1026))
+    q, k, v = _local()
+    with pytest.raises(g.UnsupportedMI355XPath, match="B=1"):
+        g.fa4_local_text_forward(q.expand(2, -1, -1, -1).contiguous(),
+                                 k.expand(2, -1, -1, -1).contiguous(),
+                                 v.expand(2, -1, -1, -1).contiguous())
+
+
+def test_local_spec_must_be_the_locked_contract(monkeypatch):
+    monkeypatch.setattr(att, "_require_gfx950", lambda _device: None)
+    with pytest.raises(g.UnsupportedMI355XPath, match="locked local"):
+        g.fa4_local_text_forward(*_local(), spec=replace(g.SLIDING_ATTENTION, softmax_scale=0.5))
+
+
+def test_vision_ids_are_validated_and_normalised(monkeypatch):
+    monkeypatch.setattr(att, "_require_gfx950", lambda _device: None)
+    q, k, v = _local(4)
+    with pytest.raises(ValueError, match="shape"):
+        g.fa4_local_forward(q, k, v, vision_block_ids=torch.zeros(1, 3, dtype=torch.int32))
+    with pytest.raises(ValueError, match="INT32 or INT64"):
+        g.fa4_local_forward(q, k, v, vision_block_ids=torch.zeros(1, 4))
+    with pytest.raises(ValueError, match="fit exactly in INT32"):
+        att._normalize_int32_metadata(torch.tensor([2**40]), name="vision_block_ids")
+    ids = att._prepare_vision_block_ids(torch.tensor([[-1, 0, 0, -1]]), q)
+    assert ids.dtype == torch.int32 and ids.shape == (4,) and ids.is_contiguous()
+
+
+def _packed(q_lengths=(2, 1), k_lengths=(3, 2)):
+    s = g.SLIDING_ATTENTION
+    q = torch.zeros(sum(q_lengths), s.num_q_heads, s.head_dim_qk, dtype=torch.bfloat16)
+    k = torch.ones(sum(k_lengths), s.num_kv_heads, s.head_dim_qk, dtype=torch.bfloat16)
+    v = torch.full_like(k, 2)
+    cq = torch.tensor([0, *torch.tensor(q_lengths).cumsum(0).tolist()], dtype=torch.int32)
+    ck = torch.tensor([0, *torch.tensor(k_lengths).cumsum(0).tolist()], dtype=torch.int32)
+    return q, k, v, cq, ck
+
+
+def test_local_varlen_validation():
+    q, k, v, cq, ck = _packed()
+    with pytest.raises(TypeError, match="Python integers"):
+        g.fa4_local_varlen_forward(q, k, v, cq, ck, max_seqlen_q=2.0, max_seqlen_k=3)
+    with pytest.raises(ValueError, match="INT32"):
+        g.fa4_local_varlen_forward(q, k, v, cq.long(), ck.long(), max_seqlen_q=2, max_seqlen_k=3)
+    with pytest.raises(ValueError, match="maxima"):
+        g.fa4_local_varlen_forward(q, k, v, cq, ck, max_seqlen_q=1, max_seqlen_k=3)
+    with pytest.raises(g.UnsupportedMI355XPath, match="Sq <= Sk"):
+        g.fa4_local_varlen_forward(*_packed((3, 1), (2, 4)), max_seqlen_q=3, max_seqlen_k=4)
+    bad = torch.tensor([0, 2, 1], dtype=torch.int32)
+    with pytest.raises(ValueError, match="end at|nondecreasing"):
+        g.fa4_local_varlen_forward(q, k, v, bad, ck, max_seqlen_q=2, max_seqlen_k=3)
+    with pytest.raises(g.UnsupportedMI355XPath, match="GPU tensors"):
+        g.fa4_local_varlen_forward(q, k, v, cq, ck, max_seqlen_q=2, max_seqlen_k=3)
+    with pytest.raises(g.UnsupportedMI355XPath, match="262144"):
+        g.fa4_local_varlen_forward(q, k, v, cq, ck, max_seqlen_q=2, max_seqlen_k=262145)
+
+
+def test_global_adapters_validation(monkeypatch):
+    monkeypatch.setattr(att, "_require_gfx950", lambda _device: None)
+    s = g.GLOBAL_ATTENTION
+    q = torch.zeros(1, 2049, 32, 512, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2049, 4, 512, dtype=torch.bfloat16)
+    v = torch.zeros(1, 2049, 4, 512, dtype=torch.bfloat16)
+    with pytest.raises(g.UnsupportedMI355XPath, match="S <= 2048"):
+        g.fa4_global_text_forward(q, k, v)
+    qg = q[:, :8].clone().requires_grad_(True)
+    with pytest.raises(g.UnsupportedMI355XPath, match="autograd"):
+        g.fa4_global_forward_only(qg, k[:, :8].clone(), v[:, :8].clone())
+    with pytest.raises(g.UnsupportedMI355XPath, match="locked global"):
+        g.fa4_global_forward_only(q[:, :8], k[:, :8], v[:, :8],
+                                  spec=replace(s, sliding_window=1024))
+
+
+def test_global_backward_budget_fails_closed():
+    free = 10 * 1024**3
+    budget = att._global_backward_budget(free)
+    assert budget == min(free * 4 // 5, free - 2 * 1024**3)
+    att._check_global_backward_budget(budget, free)
+    with pytest.raises(g.GlobalBackwardBudgetExceeded):
+        att._check_global_backward_budget(budget + 1, free)
+
+
+def test_model_contract_constants():
+    s, f = g.SLIDING_ATTENTION, g.GLOBAL_ATTENTION
+    assert (s.head_dim_qk, s.num_q_heads, s.num_kv_heads, s.sliding_window) == (256, 32, 16, 1024)
+    assert s.fa_window_size_left == 1023 and s.softmax_scale == 1.0
+    assert (f.head_dim_qk, f.num_q_heads, f.num_kv_heads, f.sliding_window) == (512, 32, 4, None)
+    types = g.GEMMA4_31B.layer_types()
+    assert len(types) == 60 and types.count("full_attention") == 10
+    assert types[5] == "full_attention" and types[4] == "sliding_attention"
+    assert f.rotary_dim == 128 and f.qhead_per_kvhead == 8 and s.qhead_per_kvhead == 2
