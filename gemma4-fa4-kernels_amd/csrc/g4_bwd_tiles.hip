@@ -1,7 +1,733 @@
-// dK/dV and dQ kernels (placeholders until the MFMA backward lands).
+// Backward MFMA kernels for gfx950: dK/dV (key-tile major) and dQ (query-tile major).
+//
+// Both recompute P = exp2(S log2e - LSE log2e) from the saved fp32 LSE and use
+// delta = rowsum(O dO) - dLSE from the pre-pass: dS = P (dP - delta), with
+// S = Q K^T and dP = dO V^T (softmax scale 1.0).  P and dS are rounded to bf16
+// before they feed the dV / dK / dQ products.  No atomics: each output element
+// is owned by one wave, so results repeat bitwise.
+//
+// dK/dV: a workgroup owns NKB * 32 keys of one KV head and loops over the
+// query heads of its GQA group and the query tiles (32 rows) the mask admits
+// (key_tile_query_range).  Lanes own keys: S and dP come out of the MFMA with
+// keys along lanes, so P and dS feed dV^T += dO^T P and dK^T += Q^T dS directly
+// from registers, with dO^T / Q^T read from the natural-layout tiles by
+// transposing LDS reads.  K and V fragments stay in VGPRs for the whole loop.
+//
+// dQ: a workgroup owns 32 * NQG queries of one query head and walks the key
+// tiles of its range like the forward: S^T = K Q^T and dP^T = V dO^T with
+// lanes owning queries, dQ^T += K^T dS^T with K^T from transposing reads.
+//
+// With DSPLIT = 2 (head dim 512) the two waves of a pair own the two halves of
+// the head dimension and exchange their partial S / dP through LDS.
 #include "g4_kernels.h"
 
 namespace g4 {
-hipError_t launch_bwd_dkdv(const BwdParams&, hipStream_t) { return hipErrorNotSupported; }
-hipError_t launch_bwd_dq(const BwdParams&, hipStream_t) { return hipErrorNotSupported; }
+
+namespace {
+
+__device__ __forceinline__ void xchg_write(char G4_LDS* xb, int slot, int lane, const f32x16& v) {
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    f32x4 w = {v[q4 * 4], v[q4 * 4 + 1], v[q4 * 4 + 2], v[q4 * 4 + 3]};
+    *(f32x4 G4_LDS*)(xb + ((slot * 4 + q4) * 64 + lane) * 16) = w;
+  }
+}
+
+// acc = (slice 0 partial) + (slice 1 partial), summed in the same order by both
+// slices so they hold bit-identical values.
+__device__ __forceinline__ void xchg_add(const char G4_LDS* xb, int slot, int lane, int dh,
+                                         f32x16& acc) {
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    f32x4 w = *(const f32x4 G4_LDS*)(xb + ((slot * 4 + q4) * 64 + lane) * 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float mine = acc[q4 * 4 + e];
+      acc[q4 * 4 + e] = dh == 0 ? mine + w[e] : w[e] + mine;
+    }
+  }
+}
+
+}  // namespace
+
+// ===========================================================================
+// dK / dV
+// ===========================================================================
+
+template <int D, int DSPLIT, int NKB>
+struct DkdvCfg {
+  static constexpr int kNW = NKB * DSPLIT;
+  static constexpr int kNT = kNW * 64;
+  static constexpr int kBN = NKB * 32;  // keys per workgroup
+  static constexpr int kBM = 32;        // queries per step
+  static constexpr int kDH = D / DSPLIT;
+  static constexpr int kCPR = D / 8;
+  static constexpr int kTile = kBM * D * 2;  // Q or dO tile bytes
+  static constexpr bool kDoDouble = DSPLIT == 1;
+  static constexpr int kXBytes = DSPLIT > 1 ? kNW * 2 * 4096 : 0;
+  static constexpr int kLdsQ = 0;
+  static constexpr int kLdsDo = kLdsQ + 2 * kTile;
+  static constexpr int kLdsX = kLdsDo + (kDoDouble ? 2 : 1) * kTile;
+  static constexpr int kLdsLd = kLdsX + kXBytes;    // [buf][lse x 32 | delta x 32] fp32
+  static constexpr int kLdsMeta = kLdsLd + 2 * 256;  // [buf][vid x 32 | doc x 32] int32
+  static constexpr int kLdsRed = kLdsMeta + 2 * 256;
+  static constexpr int kLdsBytes = kLdsRed + 64;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+};
+
+template <int D, int DSPLIT, int NKB, bool META>
+struct DkdvKernel {
+  using C = DkdvCfg<D, DSPLIT, NKB>;
+  static constexpr int kNB = C::kDH / 32;
+  static constexpr int kNC = C::kDH / 16;
+
+  char G4_LDS* smem;
+  const BwdParams* a;
+  Seq sq;
+  int s, lane, wave, dh, h32, kb;
+  int off, j0, my_j;
+  bool has_vid, has_doc, has_meta;
+  int my_vid, my_doc;
+  int grp, kvh, qt_lo, nqt;
+  int64_t tq;
+  RowReader<C::kCPR> rrd;
+  TrReader<C::kCPR> trd;
+  TileCopier<C::kCPR, 32, C::kNW> qcp, docp;
+  bf16x8 kf[kNC], vf[kNC];
+  f32x16 dk_acc[kNB], dv_acc[kNB];
+
+  // Step `it` enumerates (query head, query tile) pairs.
+  __device__ __forceinline__ void coords(int it, int& qh, int& i0) const {
+    qh = kvh * grp + it / nqt;
+    i0 = (qt_lo + it % nqt) * C::kBM;
+  }
+
+  __device__ __forceinline__ void issue_q(int it, int buf) {
+    int qh, i0;
+    coords(it, qh, i0);
+    const __bf16* base = a->q + tok_off(sq, s, sq.qtok, i0, a->ql) + (int64_t)qh * a->ql.head_stride;
+    char G4_LDS* dst = smem + C::kLdsQ + buf * C::kTile;
+    if (i0 + C::kBM <= sq.lq)
+      qcp.issue(base, dst);
+    else
+      qcp.issue_clamped(base, a->ql.token_stride, sq.lq - i0, dst, wave, lane);
+  }
+  __device__ __forceinline__ void issue_do(int it, int buf) {
+    int qh, i0;
+    coords(it, qh, i0);
+    const __bf16* base =
+        a->dout + tok_off(sq, s, sq.qtok, i0, a->dol) + (int64_t)qh * a->dol.head_stride;
+    char G4_LDS* dst = smem + C::kLdsDo + buf * C::kTile;
+    if (i0 + C::kBM <= sq.lq)
+      docp.issue(base, dst);
+    else
+      docp.issue_clamped(base, a->dol.token_stride, sq.lq - i0, dst, wave, lane);
+  }
+  // LSE (lanes 0-31) and delta (lanes 32-63) of the tile's 32 rows, and with
+  // metadata the vision / document IDs of the rows' K positions.
+  __device__ __forceinline__ void issue_rows(int it, int buf) {
+    int qh, i0;
+    coords(it, qh, i0);
+    const int i = min(i0 + (lane & 31), sq.lq - 1);
+    if (wave == 0) {
+      const float* src = lane < 32 ? a->lse + lse_off(a->p, sq, s, qh, i)
+                                   : a->delta + (int64_t)qh * tq + sq.qtok + i;
+      g2l4(src, smem + C::kLdsLd + buf * 256);
+    } else if (wave == 1 && has_meta) {
+      const int64_t kidx = sq.ktok + i + off;
+      const int* src = lane < 32 ? (has_vid ? a->p.vision_ids + kidx : a->p.document_ids + kidx)
+                                 : (has_doc ? a->p.document_ids + kidx : a->p.vision_ids + kidx);
+      g2l4(src, smem + C::kLdsMeta + buf * 256);
+    }
+  }
+
+  template <int CP>
+  __device__ __forceinline__ void sdp_step(const char G4_LDS* qt, const char G4_LDS* dot,
+                                           f32x16& sacc, f32x16& pacc) const {
+    if constexpr (CP < kNC) {
+      bf16x8 qa = rrd.template read<0, 0, CP>(qt);
+      sacc = mfma32(qa, kf[CP], sacc);
+      bf16x8 da = rrd.template read<0, 0, CP>(dot);
+      pacc = mfma32(da, vf[CP], pacc);
+      sdp_step<CP + 1>(qt, dot, sacc, pacc);
+    }
+  }
+
+  template <int M, int B>
+  __device__ __forceinline__ void acc_step(const char G4_LDS* t, const bf16x8& b, f32x16* acc) const {
+    if constexpr (B < kNB) {
+      bf16x8 x = trd.template read<16 * M, 0, B>(t);
+      acc[B] = mfma32(x, b, acc[B]);
+      acc_step<M, B + 1>(t, b, acc);
+    }
+  }
+
+  __device__ __forceinline__ void step(int cur, int it, int nsteps) {
+    int qh, i0;
+    coords(it, qh, i0);
+    // Q, dO and the row data of this step have landed (with a single dO
+    // buffer its copies were issued after the previous step's dV phase).
+    vm_wait<0>();
+    barrier_lds();
+    if (it + 1 < nsteps) {
+      issue_q(it + 1, cur ^ 1);
+      issue_rows(it + 1, cur ^ 1);
+      if constexpr (C::kDoDouble) issue_do(it + 1, cur ^ 1);
+    }
+    const char G4_LDS* qt = smem + C::kLdsQ + cur * C::kTile;
+    const char G4_LDS* dot = smem + C::kLdsDo + (C::kDoDouble ? cur : 0) * C::kTile;
+
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 sacc = {}, pacc = {};
+    sdp_step<0>(qt, dot, sacc, pacc);
+    mfma_pipeline_hint<2 * kNC, 3, 1>();
+    __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (DSPLIT > 1) {
+      char G4_LDS* xb = smem + C::kLdsX;
+      xchg_write(xb, wave * 2, lane, sacc);
+      xchg_write(xb, wave * 2 + 1, lane, pacc);
+      barrier_lds();
+      xchg_add(xb, (wave ^ 1) * 2, lane, dh, sacc);
+      xchg_add(xb, (wave ^ 1) * 2 + 1, lane, dh, pacc);
+    }
+
+    // Rows (queries) of the accumulators: 8 (r >> 2) + 4 h32 + (r & 3).
+    const float* ld = (const float*)(smem + C::kLdsLd + cur * 256);
+    const bool full = !has_doc && (i0 + C::kBM <= sq.lq) && (j0 + C::kBN <= sq.lk) &&
+                      (j0 + C::kBN - 1 <= i0 + off) &&
+                      (a->p.window <= 0 || j0 > i0 + C::kBM - 1 + off - a->p.window);
+    bf16x8 pb[2], db[2];
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int il0 = 8 * r4 + 4 * h32;
+      const f32x4 lse4 = *(const f32x4*)(ld + il0);
+      const f32x4 del4 = *(const f32x4*)(ld + 32 + il0);
+      i32x4 vq4 = {-1, -1, -1, -1}, dq4 = {0, 0, 0, 0};
+      if (has_meta && !full) {
+        const int* mt = (const int*)(smem + C::kLdsMeta + cur * 256);
+        vq4 = *(const i32x4*)(mt + il0);
+        dq4 = *(const i32x4*)(mt + 32 + il0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = r4 * 4 + e;
+        float p = fast_exp2(sacc[r] * kLog2e - lse4[e] * kLog2e);
+        if (!full) {
+          const int i = i0 + il0 + e;
+          const int aq = i + off;
+          const bool in_w = a->p.window <= 0 || my_j > aq - a->p.window;
+          const bool causal = my_j <= aq;
+          const bool vis = has_vid & (vq4[e] >= 0) & (vq4[e] == my_vid);
+          const bool doc_ok = !has_doc | (dq4[e] == my_doc);
+          const bool ok = (i < sq.lq) & (my_j < sq.lk) & in_w & (causal | vis) & doc_ok;
+          p = ok ? p : 0.f;
+        }
+        const float ds = p * (pacc[r] - del4[e]);
+        pb[r >> 3][r & 7] = (__bf16)p;
+        db[r >> 3][r & 7] = (__bf16)ds;
+      }
+    }
+
+    __builtin_amdgcn_sched_barrier(0);
+    acc_step<0, 0>(dot, pb[0], dv_acc);
+    acc_step<1, 0>(dot, pb[1], dv_acc);
+    mfma_pipeline_hint<2 * kNB, 6, 2>();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!C::kDoDouble) {
+      // Single dO buffer: refill once every wave finished its dV reads.
+      barrier_lds();
+      if (it + 1 < nsteps) issue_do(it + 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    acc_step<0, 0>(qt, db[0], dk_acc);
+    acc_step<1, 0>(qt, db[1], dk_acc);
+    mfma_pipeline_hint<2 * kNB, 6, 2>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+};
+
+template <int D, int DSPLIT, int NKB, bool META>
+__global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a) {
+  using K = DkdvKernel<D, DSPLIT, NKB, META>;
+  using C = typename K::C;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  K ker;
+  ker.smem = (char G4_LDS*)smem_raw;
+  ker.a = &a;
+  const g4_problem& p = a.p;
+  const int tid = threadIdx.x;
+  ker.lane = tid & 63;
+  ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  ker.kb = ker.wave / DSPLIT;
+  ker.dh = ker.wave % DSPLIT;
+  ker.h32 = ker.lane >> 5;
+  const int l32 = ker.lane & 31;
+
+  // ---- work item: (sequence, key tile, KV head) ------------------------------
+  ker.grp = p.num_q_heads / p.num_kv_heads;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_kvh = a.num_seqs * a.ntiles;
+  ker.kvh = L / per_kvh;
+  const int rank = L % per_kvh;
+  ker.s = rank / a.ntiles;
+  const int kt = zigzag(rank % a.ntiles, a.ntiles);
+  ker.sq = resolve_seq(p, ker.s);
+  const Seq& sq = ker.sq;
+  ker.j0 = kt * C::kBN;
+  if (ker.j0 >= sq.lk) return;
+  ker.off = sq.lk - sq.lq;
+  ker.tq = q_stream_tokens_dev(p);
+  ker.has_vid = META && p.vision_ids != nullptr && p.bidirectional_vision;
+  ker.has_doc = META && p.document_ids != nullptr;
+  ker.has_meta = ker.has_vid || ker.has_doc;
+  const int j_last = min(ker.j0 + C::kBN, sq.lk) - 1;
+  ker.my_j = ker.j0 + ker.kb * 32 + l32;
+  const int jc = min(ker.my_j, sq.lk - 1);
+
+  // ---- query range of this key tile ---------------------------------------
+  int span_min = 0x7fffffff;
+  if (ker.has_vid) {
+    int* red = (int*)(smem_raw + C::kLdsRed);
+    int v = 0x7fffffff;
+    for (int t = tid; t < C::kBN; t += C::kNT) {
+      int j = ker.j0 + t;
+      if (j < sq.lk) v = min(v, a.span_lo[sq.ktok + j]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+    if (ker.lane == 0) red[ker.wave] = v;
+    barrier_lds();
+#pragma unroll
+    for (int w = 0; w < C::kNW; ++w) span_min = min(span_min, red[w]);
+  }
+  int ilo, ihi;
+  key_tile_query_range(ker.j0, j_last, sq.lq, ker.off, p.window, span_min, ilo, ihi);
+  ker.qt_lo = ilo / C::kBM;
+  ker.nqt = ihi > ilo ? (ihi + C::kBM - 1) / C::kBM - ker.qt_lo : 0;
+  const int nsteps = ker.nqt * ker.grp;
+
+  ker.rrd.init(ker.lane, ker.dh * C::kDH * 2);
+  ker.trd.init(ker.lane, ker.dh * C::kDH * 2);
+  ker.qcp.init(a.ql.token_stride, ker.wave, ker.lane);
+  ker.docp.init(a.dol.token_stride, ker.wave, ker.lane);
+
+  // ---- K / V fragments of this wave's 32 keys (B operands) ---------------
+  {
+    const __bf16* krow = a.k + tok_off(sq, ker.s, sq.ktok, jc, a.kl) +
+                         (int64_t)ker.kvh * a.kl.head_stride + ker.dh * C::kDH + ker.h32 * 8;
+    const __bf16* vrow = a.v + tok_off(sq, ker.s, sq.ktok, jc, a.vl) +
+                         (int64_t)ker.kvh * a.vl.head_stride + ker.dh * C::kDH + ker.h32 * 8;
+#pragma unroll
+    for (int c = 0; c < K::kNC; ++c) {
+      ker.kf[c] = ld_global16(krow + c * 16);
+      ker.vf[c] = ld_global16(vrow + c * 16);
+    }
+  }
+  ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + jc] : -1;
+  ker.my_doc = ker.has_doc ? p.document_ids[sq.ktok + jc] : 0;
+
+#pragma unroll
+  for (int b = 0; b < K::kNB; ++b) {
+    ker.dk_acc[b] = f32x16{};
+    ker.dv_acc[b] = f32x16{};
+  }
+
+  if (nsteps > 0) {
+    ker.issue_q(0, 0);
+    ker.issue_rows(0, 0);
+    ker.issue_do(0, 0);
+  }
+  for (int it = 0; it < nsteps; ++it) {
+    ker.step(it & 1, it, nsteps);
+  }
+
+  // ---- write dK, dV (bf16), 4 consecutive head-dim elements per store --------
+  if (ker.my_j < sq.lk) {
+    __bf16* dkrow = a.dk + tok_off(sq, ker.s, sq.ktok, ker.my_j, a.dkl) +
+                    (int64_t)ker.kvh * a.dkl.head_stride;
+    __bf16* dvrow = a.dv + tok_off(sq, ker.s, sq.ktok, ker.my_j, a.dvl) +
+                    (int64_t)ker.kvh * a.dvl.head_stride;
+#pragma unroll
+    for (int b = 0; b < K::kNB; ++b)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = ker.dh * C::kDH + b * 32 + 8 * r4 + 4 * ker.h32;
+        const f32x16& x = ker.dk_acc[b];
+        const f32x16& y = ker.dv_acc[b];
+        *(bf16x4*)(dkrow + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
+                                       (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
+        *(bf16x4*)(dvrow + d) = bf16x4{(__bf16)y[r4 * 4], (__bf16)y[r4 * 4 + 1],
+                                       (__bf16)y[r4 * 4 + 2], (__bf16)y[r4 * 4 + 3]};
+      }
+  }
+}
+
+// ===========================================================================
+// dQ
+// ===========================================================================
+
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE>
+struct DqCfg {
+  static constexpr int kNW = NQG * DSPLIT;
+  static constexpr int kNT = kNW * 64;
+  static constexpr int kBM = NQG * 32;
+  static constexpr int kDH = D / DSPLIT;
+  static constexpr int kCPR = D / 8;
+  static constexpr int kTile = BN * D * 2;
+  static constexpr int kKB = BN / 32;
+  static constexpr int kXBytes = DSPLIT > 1 ? kNW * kKB * 2 * 4096 : 0;
+  static constexpr int kLdsK = 0;
+  static constexpr int kLdsV = kLdsK + 2 * kTile;
+  static constexpr int kLdsX = kLdsV + (VDOUBLE ? 2 : 1) * kTile;
+  static constexpr int kLdsMeta = kLdsX + kXBytes;  // [buf][vid x 64 | doc x 64] int32
+  static constexpr int kLdsRed = kLdsMeta + 2 * 512;
+  static constexpr int kLdsBytes = kLdsRed + 64;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+};
+
+__device__ __forceinline__ void issue_key_meta(const g4_problem& p, const Seq& sq, int j0,
+                                               char G4_LDS* dst, int lane) {
+  const int64_t idx = sq.ktok + min(j0 + lane, sq.lk - 1);
+  if (p.vision_ids != nullptr && p.bidirectional_vision) g2l4(p.vision_ids + idx, dst);
+  if (p.document_ids != nullptr) g2l4(p.document_ids + idx, dst + 256);
+}
+
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META>
+struct DqKernel {
+  using C = DqCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
+  static constexpr int kNB = C::kDH / 32;
+  static constexpr int kNC = C::kDH / 16;
+
+  char G4_LDS* smem;
+  const BwdParams* a;
+  Seq sq;
+  int lane, wave, dh, h32;
+  int my_a, my_vid, my_doc, a0;
+  bool has_vid, has_doc, has_meta, q_valid;
+  float my_lse2, my_delta;
+  const __bf16* kbase;
+  const __bf16* vbase;
+  int64_t kstride, vstride;
+  RowReader<C::kCPR> rrd;
+  TrReader<C::kCPR> trd;
+  TileCopier<C::kCPR, BN, C::kNW> kcp, vcp;
+  bf16x8 qf[kNC], gf[kNC];
+  f32x16 dq_acc[kNB];
+
+  __device__ __forceinline__ void issue_k(int row0, int buf) {
+    char G4_LDS* dst = smem + C::kLdsK + buf * C::kTile;
+    if (row0 + BN <= sq.lk)
+      kcp.issue(kbase + row0 * kstride, dst);
+    else
+      kcp.issue_clamped(kbase + row0 * kstride, kstride, sq.lk - row0, dst, wave, lane);
+  }
+  __device__ __forceinline__ void issue_v(int row0, int buf) {
+    char G4_LDS* dst = smem + C::kLdsV + buf * C::kTile;
+    if (row0 + BN <= sq.lk)
+      vcp.issue(vbase + row0 * vstride, dst);
+    else
+      vcp.issue_clamped(vbase + row0 * vstride, vstride, sq.lk - row0, dst, wave, lane);
+  }
+
+  template <int KB, int CP>
+  __device__ __forceinline__ void sdp_step(const char G4_LDS* kt, const char G4_LDS* vt,
+                                           f32x16& sacc, f32x16& pacc) const {
+    if constexpr (CP < kNC) {
+      bf16x8 ka = rrd.template read<KB * 32, 0, CP>(kt);
+      sacc = mfma32(ka, qf[CP], sacc);
+      bf16x8 va = rrd.template read<KB * 32, 0, CP>(vt);
+      pacc = mfma32(va, gf[CP], pacc);
+      sdp_step<KB, CP + 1>(kt, vt, sacc, pacc);
+    }
+  }
+
+  template <int KB, int HK, int B>
+  __device__ __forceinline__ void dq_step(const char G4_LDS* kt, const bf16x8& ds) {
+    if constexpr (B < kNB) {
+      bf16x8 x = trd.template read<KB * 32 + 16 * HK, 0, B>(kt);
+      dq_acc[B] = mfma32(x, ds, dq_acc[B]);
+      dq_step<KB, HK, B + 1>(kt, ds);
+    }
+  }
+
+  __device__ __forceinline__ void step(int cur, int it, int ntiles, int t_first) {
+    const int kb0 = (t_first + it) * BN;
+    constexpr int kPer = decltype(kcp)::kPer;
+    if constexpr (VDOUBLE)
+      vm_wait<0>();
+    else
+      vm_wait<kPer>();
+    barrier_lds();
+    if (it + 1 < ntiles) {
+      issue_k(kb0 + BN, cur ^ 1);
+      if (has_meta && wave == 0)
+        issue_key_meta(a->p, sq, kb0 + BN, smem + C::kLdsMeta + (cur ^ 1) * 512, lane);
+      if constexpr (VDOUBLE) issue_v(kb0 + BN, cur ^ 1);
+    }
+    const char G4_LDS* kt = smem + C::kLdsK + cur * C::kTile;
+    const char G4_LDS* vt = smem + C::kLdsV + (VDOUBLE ? cur : 0) * C::kTile;
+    if constexpr (!VDOUBLE) {
+      // This tile's V copies were issued after the previous step's exchange.
+      vm_wait<kPer>();
+      barrier_lds();
+    }
+
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 sacc[C::kKB], pacc[C::kKB];
+    sacc[0] = f32x16{};
+    pacc[0] = f32x16{};
+    sdp_step<0, 0>(kt, vt, sacc[0], pacc[0]);
+    if constexpr (C::kKB > 1) {
+      sacc[1] = f32x16{};
+      pacc[1] = f32x16{};
+      sdp_step<1, 0>(kt, vt, sacc[1], pacc[1]);
+    }
+    mfma_pipeline_hint<2 * C::kKB * kNC, 3, 1>();
+    __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (DSPLIT > 1) {
+      char G4_LDS* xb = smem + C::kLdsX;
+#pragma unroll
+      for (int kb = 0; kb < C::kKB; ++kb) {
+        xchg_write(xb, (wave * C::kKB + kb) * 2, lane, sacc[kb]);
+        xchg_write(xb, (wave * C::kKB + kb) * 2 + 1, lane, pacc[kb]);
+      }
+      barrier_lds();
+#pragma unroll
+      for (int kb = 0; kb < C::kKB; ++kb) {
+        xchg_add(xb, ((wave ^ 1) * C::kKB + kb) * 2, lane, dh, sacc[kb]);
+        xchg_add(xb, ((wave ^ 1) * C::kKB + kb) * 2 + 1, lane, dh, pacc[kb]);
+      }
+    }
+    if constexpr (!VDOUBLE) {
+      // Every wave is past its V reads (the exchange barrier, or the one
+      // below without an exchange): refill the single V buffer.
+      if constexpr (DSPLIT == 1) barrier_lds();
+      if (it + 1 < ntiles) issue_v(kb0 + BN, 0);
+    }
+
+    const bool full = !has_doc && (kb0 + BN <= sq.lk) && (kb0 + BN - 1 <= a0) &&
+                      (a->p.window <= 0 || kb0 > a0 + C::kBM - 1 - a->p.window);
+    const int lo_w = a->p.window > 0 ? my_a - a->p.window + 1 : -0x40000000;
+    const int hi_c = min(my_a, sq.lk - 1);
+    const int* km = (const int*)(smem + C::kLdsMeta + cur * 512);
+    bf16x8 dsb[C::kKB][2];
+#pragma unroll
+    for (int kb = 0; kb < C::kKB; ++kb)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int jl0 = kb * 32 + 8 * r4 + 4 * h32;
+        i32x4 vk = {-1, -1, -1, -1}, dk = {0, 0, 0, 0};
+        if (has_meta && !full) {
+          vk = *(const i32x4*)(km + jl0);
+          dk = *(const i32x4*)(km + 64 + jl0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = r4 * 4 + e;
+          float p = fast_exp2(sacc[kb][r] * kLog2e - my_lse2);
+          if (!full) {
+            const int j = kb0 + jl0 + e;
+            const bool in_w = j >= lo_w;
+            const bool causal = in_w & (j <= hi_c);
+            const bool vis = has_vid & (my_vid >= 0) & (vk[e] == my_vid) & in_w & (j < sq.lk);
+            const bool doc_ok = !has_doc | (dk[e] == my_doc);
+            p = ((causal | vis) & doc_ok & q_valid) ? p : 0.f;
+          }
+          dsb[kb][r >> 3][r & 7] = (__bf16)(p * (pacc[kb][r] - my_delta));
+        }
+      }
+
+    __builtin_amdgcn_sched_barrier(0);
+    dq_step<0, 0, 0>(kt, dsb[0][0]);
+    dq_step<0, 1, 0>(kt, dsb[0][1]);
+    if constexpr (C::kKB > 1) {
+      dq_step<1, 0, 0>(kt, dsb[1][0]);
+      dq_step<1, 1, 0>(kt, dsb[1][1]);
+    }
+    mfma_pipeline_hint<C::kKB * 2 * kNB, 6, 2>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+};
+
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META>
+__global__ void __launch_bounds__(NQG * DSPLIT * 64, 1) dq_kernel(BwdParams a) {
+  using K = DqKernel<D, BN, DSPLIT, NQG, VDOUBLE, META>;
+  using C = typename K::C;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  K ker;
+  ker.smem = (char G4_LDS*)smem_raw;
+  ker.a = &a;
+  const g4_problem& p = a.p;
+  const int tid = threadIdx.x;
+  ker.lane = tid & 63;
+  ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qg = ker.wave / DSPLIT;
+  ker.dh = ker.wave % DSPLIT;
+  ker.h32 = ker.lane >> 5;
+  const int l32 = ker.lane & 31;
+
+  const int grp = p.num_q_heads / p.num_kv_heads;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_kvh = a.num_seqs * a.ntiles * grp;
+  const int kvh = L / per_kvh;
+  const int rem = L % per_kvh;
+  const int rank = rem / grp;
+  const int qh = kvh * grp + rem % grp;
+  const int s = rank / a.ntiles;
+  const int qt = zigzag(rank % a.ntiles, a.ntiles);
+  ker.sq = resolve_seq(p, s);
+  const Seq& sq = ker.sq;
+  const int i0 = qt * C::kBM;
+  if (i0 >= sq.lq) return;
+  const int off = sq.lk - sq.lq;
+  ker.a0 = i0 + off;
+  const int a_last_valid = min(i0 + C::kBM, sq.lq) - 1 + off;
+  ker.has_vid = META && p.vision_ids != nullptr && p.bidirectional_vision;
+  ker.has_doc = META && p.document_ids != nullptr;
+  ker.has_meta = ker.has_vid || ker.has_doc;
+
+  int span_max = -1;
+  if (ker.has_vid) {
+    int* red = (int*)(smem_raw + C::kLdsRed);
+    int v = -1;
+    for (int t = tid; t < C::kBM; t += C::kNT) {
+      int i = i0 + t;
+      if (i < sq.lq) v = max(v, a.span_hi[sq.ktok + i + off]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+    if (ker.lane == 0) red[ker.wave] = v;
+    barrier_lds();
+#pragma unroll
+    for (int w = 0; w < C::kNW; ++w) span_max = max(span_max, red[w]);
+  }
+  int klo, khi;
+  query_tile_key_range(ker.a0, a_last_valid, sq.lk, p.window, span_max, klo, khi);
+  const int t_first = klo / BN;
+  const int ntiles = (khi + BN - 1) / BN - t_first;
+
+  ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
+  ker.vbase = a.v + tok_off(sq, s, sq.ktok, 0, a.vl) + (int64_t)kvh * a.vl.head_stride;
+  ker.kstride = a.kl.token_stride;
+  ker.vstride = a.vl.token_stride;
+  ker.rrd.init(ker.lane, ker.dh * C::kDH * 2);
+  ker.trd.init(ker.lane, ker.dh * C::kDH * 2);
+  ker.kcp.init(ker.kstride, ker.wave, ker.lane);
+  ker.vcp.init(ker.vstride, ker.wave, ker.lane);
+
+  const int my_i = i0 + qg * 32 + l32;
+  ker.my_a = my_i + off;
+  ker.q_valid = my_i < sq.lq;
+  const int ic = min(my_i, sq.lq - 1);
+  {
+    const __bf16* qrow = a.q + tok_off(sq, s, sq.qtok, ic, a.ql) + (int64_t)qh * a.ql.head_stride +
+                         ker.dh * C::kDH + ker.h32 * 8;
+    const __bf16* grow = a.dout + tok_off(sq, s, sq.qtok, ic, a.dol) +
+                         (int64_t)qh * a.dol.head_stride + ker.dh * C::kDH + ker.h32 * 8;
+#pragma unroll
+    for (int c = 0; c < K::kNC; ++c) {
+      ker.qf[c] = ld_global16(qrow + c * 16);
+      ker.gf[c] = ld_global16(grow + c * 16);
+    }
+  }
+  ker.my_lse2 = a.lse[lse_off(p, sq, s, qh, ic)] * kLog2e;
+  ker.my_delta = a.delta[(int64_t)qh * q_stream_tokens_dev(p) + sq.qtok + ic];
+  ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + ic + off] : -1;
+  ker.my_doc = ker.has_doc ? p.document_ids[sq.ktok + ic + off] : 0;
+
+#pragma unroll
+  for (int b = 0; b < K::kNB; ++b) ker.dq_acc[b] = f32x16{};
+
+  if (ntiles > 0) {
+    ker.issue_k(t_first * BN, 0);
+    if (ker.has_meta && ker.wave == 0)
+      issue_key_meta(p, sq, t_first * BN, ker.smem + C::kLdsMeta, ker.lane);
+    ker.issue_v(t_first * BN, 0);
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    ker.step(it & 1, it, ntiles, t_first);
+  }
+
+  if (ker.q_valid) {
+    __bf16* row = a.dq + tok_off(sq, s, sq.qtok, my_i, a.dql) + (int64_t)qh * a.dql.head_stride;
+#pragma unroll
+    for (int b = 0; b < K::kNB; ++b)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = ker.dh * C::kDH + b * 32 + 8 * r4 + 4 * ker.h32;
+        const f32x16& x = ker.dq_acc[b];
+        *(bf16x4*)(row + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
+                                     (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
+      }
+  }
+}
+
+// ===========================================================================
+// launchers
+// ===========================================================================
+
+namespace {
+
+bool has_meta(const g4_problem& p) {
+  return (p.vision_ids != nullptr && p.bidirectional_vision) || p.document_ids != nullptr;
+}
+
+template <typename Kern>
+hipError_t set_lds(Kern kern, int bytes, bool& done) {
+  if (done) return hipSuccess;
+  hipError_t e =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done = true;
+  return e;
+}
+
+template <int D, int DSPLIT, int NKB>
+hipError_t launch_dkdv_cfg(const BwdParams& a, hipStream_t stream) {
+  using C = DkdvCfg<D, DSPLIT, NKB>;
+  const bool meta = has_meta(a.p);
+  auto kern = meta ? dkdv_kernel<D, DSPLIT, NKB, true> : dkdv_kernel<D, DSPLIT, NKB, false>;
+  static bool done[2] = {false, false};
+  hipError_t e = set_lds(kern, C::kLdsBytes, done[meta]);
+  if (e != hipSuccess) return e;
+  BwdParams b = a;
+  b.ntiles = (a.p.seqlen_k + C::kBN - 1) / C::kBN;
+  const int64_t nblocks = (int64_t)b.num_seqs * b.ntiles * a.p.num_kv_heads;
+  if (nblocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
+  return hipGetLastError();
+}
+
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE>
+hipError_t launch_dq_cfg(const BwdParams& a, hipStream_t stream) {
+  using C = DqCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
+  const bool meta = has_meta(a.p);
+  auto kern = meta ? dq_kernel<D, BN, DSPLIT, NQG, VDOUBLE, true>
+                   : dq_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false>;
+  static bool done[2] = {false, false};
+  hipError_t e = set_lds(kern, C::kLdsBytes, done[meta]);
+  if (e != hipSuccess) return e;
+  BwdParams b = a;
+  b.ntiles = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
+  const int64_t nblocks = (int64_t)b.num_seqs * b.ntiles * a.p.num_q_heads;
+  if (nblocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_bwd_dkdv(const BwdParams& a, hipStream_t stream) {
+  if (a.p.head_dim == 256) return launch_dkdv_cfg<256, 1, 4>(a, stream);
+  if (a.p.head_dim == 512) return launch_dkdv_cfg<512, 2, 2>(a, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_bwd_dq(const BwdParams& a, hipStream_t stream) {
+  if (a.p.head_dim == 256) return launch_dq_cfg<256, 64, 1, 4, true>(a, stream);
+  if (a.p.head_dim == 512) return launch_dq_cfg<512, 32, 2, 2, false>(a, stream);
+  return hipErrorInvalidValue;
+}
+
 }  // namespace g4

@@ -106,11 +106,13 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 template <int CPR>
 struct RowReader {
   int off[8];
-  __device__ __forceinline__ void init(int lane) {
+  // base: byte offset added to every read (e.g. the wave's head-dim slice,
+  // 16 * a multiple of 16 chunks), folded in here so reads are reg + immediate.
+  __device__ __forceinline__ void init(int lane, int base = 0) {
     const int r = lane & 31, h = lane >> 5;
     const int sw = ((r & 3) << 2) | ((r >> 2) & 3);
 #pragma unroll
-    for (int w = 0; w < 8; ++w) off[w] = (r * CPR + ((2 * w + h) ^ sw)) * 16;
+    for (int w = 0; w < 8; ++w) off[w] = base + (r * CPR + ((2 * w + h) ^ sw)) * 16;
   }
   template <int ROW0, int CBASE, int CP>
   __device__ __forceinline__ bf16x8 read(const char G4_LDS* tile) const {
@@ -126,7 +128,7 @@ struct RowReader {
 template <int CPR>
 struct TrReader {
   int off[2][4];
-  __device__ __forceinline__ void init(int lane) {
+  __device__ __forceinline__ void init(int lane, int base = 0) {
     const int g = lane >> 4, sl = lane & 15;
     const int rl = 4 * (g >> 1) + (sl >> 2);
     const int lb = 2 * (g & 1) + ((sl >> 1) & 1);
@@ -136,7 +138,7 @@ struct TrReader {
       const int r = rl + 8 * e;
       const int sw = ((r & 3) << 2) | ((r >> 2) & 3);
 #pragma unroll
-      for (int bq = 0; bq < 4; ++bq) off[e][bq] = (r * CPR + ((4 * bq + lb) ^ sw)) * 16 + half;
+      for (int bq = 0; bq < 4; ++bq) off[e][bq] = base + (r * CPR + ((4 * bq + lb) ^ sw)) * 16 + half;
     }
   }
   template <int ROW0, int CBASE, int B>
@@ -242,6 +244,11 @@ __device__ __forceinline__ int64_t tok_off(const Seq& sq, int s, int64_t seq_tok
                                            const g4_layout& L) {
   return sq.packed ? (seq_tok0 + t) * L.token_stride
                    : (int64_t)s * L.batch_stride + (int64_t)t * L.token_stride;
+}
+
+// Tokens in the Q stream (packed total, or num_seqs * seqlen_q).
+__device__ __forceinline__ int64_t q_stream_tokens_dev(const g4_problem& p) {
+  return p.cu_seqlens_q ? p.total_q : (int64_t)p.num_seqs * p.seqlen_q;
 }
 
 // LSE / delta element offset for (s, h, local token i).

@@ -89,7 +89,7 @@ struct FwdKernel {
   __device__ __forceinline__ void s_step(const char G4_LDS* kt, f32x16& acc) const {
     if constexpr (CP < kNC) {
       // slice dh starts at chunk dh * kDH / 8 (a multiple of 16)
-      bf16x8 kf = krd.template read<KB * 32, 0, CP>(kt + dh * C::kDH * 2);
+      bf16x8 kf = krd.template read<KB * 32, 0, CP>(kt);
       acc = mfma32(kf, qf[CP], acc);
       s_step<KB, CP + 1>(kt, acc);
     }
@@ -98,7 +98,7 @@ struct FwdKernel {
   template <int KB, int HK, int B>
   __device__ __forceinline__ void pv_step(const char G4_LDS* vt, const bf16x8& pb) {
     if constexpr (B < kNB) {
-      bf16x8 vf = vrd.template read<KB * 32 + 16 * HK, 0, B>(vt + dh * C::kDH * 2);
+      bf16x8 vf = vrd.template read<KB * 32 + 16 * HK, 0, B>(vt);
       o_acc[B] = mfma32(vf, pb, o_acc[B]);
       pv_step<KB, HK, B + 1>(vt, pb);
     }
@@ -107,11 +107,10 @@ struct FwdKernel {
   // Branch-free Gemma predicate on the lane's 16 * kKB scores (keys kb0 + ...).
   // Causal part: lo_w <= j <= min(a, Sk - 1); vision part: same non-negative
   // block, j >= lo_w, j < Sk; document part: equal IDs.
-  template <int CUR>
-  __device__ __forceinline__ void apply_mask(f32x16 (&sacc)[C::kKB], int kb0) const {
+  __device__ __forceinline__ void apply_mask(int cur, f32x16 (&sacc)[C::kKB], int kb0) const {
     const int lo_w = p->window > 0 ? my_a - p->window + 1 : -0x40000000;
     const int hi_c = min(my_a, sq.lk - 1);
-    const int* km = (const int*)(smem + C::kLdsMeta + CUR * 512);
+    const int* km = (const int*)(smem + C::kLdsMeta + cur * 512);
 #pragma unroll
     for (int kb = 0; kb < C::kKB; ++kb)
 #pragma unroll
@@ -135,8 +134,7 @@ struct FwdKernel {
       }
   }
 
-  template <int CUR>
-  __device__ __forceinline__ void step(int it, int ntiles, int t_first) {
+  __device__ __forceinline__ void step(int cur, int it, int ntiles, int t_first) {
     const int kb0 = (t_first + it) * BN;
     // This wave's copies of K (and, double-buffered, V) for this tile have
     // landed; the barrier publishes every wave's copies and ends all reads of
@@ -147,14 +145,14 @@ struct FwdKernel {
       vm_wait<C::kLoadsPerWave>();
     barrier_lds();
     if (it + 1 < ntiles) {
-      issue_k(kb0 + BN, CUR ^ 1);
-      if (has_meta && wave == 0) issue_meta(*p, sq, kb0 + BN, smem + C::kLdsMeta + (CUR ^ 1) * 512, lane);
-      if constexpr (VDOUBLE) issue_v(kb0 + BN, CUR ^ 1);
+      issue_k(kb0 + BN, cur ^ 1);
+      if (has_meta && wave == 0) issue_meta(*p, sq, kb0 + BN, smem + C::kLdsMeta + (cur ^ 1) * 512, lane);
+      if constexpr (VDOUBLE) issue_v(kb0 + BN, cur ^ 1);
     }
 
     // S^T partial over this wave's head-dim slice.
     f32x16 sacc[C::kKB];
-    const char G4_LDS* kt = smem + C::kLdsK + CUR * C::kTileBytes;
+    const char G4_LDS* kt = smem + C::kLdsK + cur * C::kTileBytes;
     __builtin_amdgcn_sched_barrier(0);
     sacc[0] = f32x16{};
     s_step<0, 0>(kt, sacc[0]);
@@ -207,7 +205,7 @@ struct FwdKernel {
     for (int kb = 0; kb < C::kKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[kb][r] *= kLog2e;
-    if (!full) apply_mask<CUR>(sacc, kb0);
+    if (!full) apply_mask(cur, sacc, kb0);
     float mx = kNegInf;
 #pragma unroll
     for (int kb = 0; kb < C::kKB; ++kb)
@@ -237,7 +235,7 @@ struct FwdKernel {
     }
 
     // O^T += V^T P^T with V^T from transposing reads of the V tile.
-    const char G4_LDS* vt = smem + C::kLdsV + (VDOUBLE ? CUR : 0) * C::kTileBytes;
+    const char G4_LDS* vt = smem + C::kLdsV + (VDOUBLE ? cur : 0) * C::kTileBytes;
     __builtin_amdgcn_sched_barrier(0);
     pv_step<0, 0, 0>(vt, pb[0][0]);
     pv_step<0, 1, 0>(vt, pb[0][1]);
@@ -322,8 +320,8 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, 1) fwd_kernel(FwdParams a) 
   ker.vbase = a.v + tok_off(sq, s, sq.ktok, 0, a.vl) + (int64_t)kvh * a.vl.head_stride;
   ker.kstride = a.kl.token_stride;
   ker.vstride = a.vl.token_stride;
-  ker.krd.init(ker.lane);
-  ker.vrd.init(ker.lane);
+  ker.krd.init(ker.lane, ker.dh * C::kDH * 2);
+  ker.vrd.init(ker.lane, ker.dh * C::kDH * 2);
   ker.kcp.init(ker.kstride, ker.wave, ker.lane);
   ker.vcp.init(ker.vstride, ker.wave, ker.lane);
 
@@ -357,9 +355,8 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, 1) fwd_kernel(FwdParams a) 
   ker.m_run = kNegInf;
   ker.l_run = 0.f;
 
-  for (int it = 0; it < ntiles; it += 2) {
-    ker.template step<0>(it, ntiles, t_first);
-    if (it + 1 < ntiles) ker.template step<1>(it + 1, ntiles, t_first);
+  for (int it = 0; it < ntiles; ++it) {
+    ker.step(it & 1, it, ntiles, t_first);
   }
 
   // ---- epilogue: normalise, write O and LSE ---------------------------------
