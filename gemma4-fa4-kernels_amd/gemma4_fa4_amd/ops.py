@@ -80,3 +80,62 @@ def tile_ranges(plan: _Plan, direction: int, row_tile: int, device) -> torch.Ten
             )
         )
     return out
+
+
+class Stages:
+    """The forward kernel and the three backward stages as separate launches.
+
+    Used to time each kernel on its own stream position (the adapters launch
+    them back to back).  Buffers are allocated once; every call is a single
+    stream-ordered library call on the current stream.
+    """
+
+    def __init__(self, plan: _Plan, q, k, v, dout, dlse=None):
+        from .attention import _layout
+
+        self.plan = plan
+        self.q, self.k, self.v, self.dout, self.dlse = q, k, v, dout, dlse
+        dev = q.device
+        self.o = torch.empty_like(q)
+        self.lse = torch.empty(plan.lse_shape(), dtype=torch.float32, device=dev)
+        self.dq = torch.empty_like(q)
+        self.dk = torch.empty_like(k)
+        self.dv = torch.empty_like(v)
+        self.ws = torch.empty(max(plan.workspace_bytes(1), 256), dtype=torch.uint8, device=dev)
+        self.prob = plan.problem()
+        self.lay = {name: _layout(t, plan.packed) for name, t in (
+            ("q", q), ("k", k), ("v", v), ("o", self.o), ("do", dout), ("dq", self.dq),
+            ("dk", self.dk), ("dv", self.dv))}
+        self.lib = _lib.load()
+
+    def _stream(self):
+        return torch.cuda.current_stream(self.q.device).cuda_stream
+
+    def forward(self):
+        L = self.lay
+        _lib.check(self.lib.g4_attn_fwd(
+            ctypes.byref(self.prob), self.q.data_ptr(), L["q"], self.k.data_ptr(), L["k"],
+            self.v.data_ptr(), L["v"], self.o.data_ptr(), L["o"], self.lse.data_ptr(),
+            self.ws.data_ptr(), self.ws.numel(), self._stream()))
+
+    def delta(self):
+        L = self.lay
+        _lib.check(self.lib.g4_attn_bwd_delta(
+            ctypes.byref(self.prob), self.o.data_ptr(), L["o"], self.dout.data_ptr(), L["do"],
+            None if self.dlse is None else self.dlse.data_ptr(), self.ws.data_ptr(),
+            self.ws.numel(), self._stream()))
+
+    def dkdv(self):
+        L = self.lay
+        _lib.check(self.lib.g4_attn_bwd_dkdv(
+            ctypes.byref(self.prob), self.q.data_ptr(), L["q"], self.k.data_ptr(), L["k"],
+            self.v.data_ptr(), L["v"], self.dout.data_ptr(), L["do"], self.lse.data_ptr(),
+            self.dk.data_ptr(), L["dk"], self.dv.data_ptr(), L["dv"], self.ws.data_ptr(),
+            self.ws.numel(), self._stream()))
+
+    def dq_stage(self):
+        L = self.lay
+        _lib.check(self.lib.g4_attn_bwd_dq(
+            ctypes.byref(self.prob), self.q.data_ptr(), L["q"], self.k.data_ptr(), L["k"],
+            self.v.data_ptr(), L["v"], self.dout.data_ptr(), L["do"], self.lse.data_ptr(),
+            self.dq.data_ptr(), L["dq"], self.ws.data_ptr(), self.ws.numel(), self._stream()))
