@@ -32,6 +32,11 @@ int check_problem(const g4_problem* p) {
   if (p->num_seqs < 1) return fail(G4_ERR_INVALID, "num_seqs must be >= 1");
   if (p->num_q_heads < 1 || p->num_kv_heads < 1 || p->num_q_heads % p->num_kv_heads)
     return fail(G4_ERR_INVALID, "num_q_heads must be a positive multiple of num_kv_heads");
+  {
+    const int grp = p->num_q_heads / p->num_kv_heads;
+    if (grp != 1 && grp != 2 && grp != 4 && grp != 8)
+      return fail(G4_ERR_UNSUPPORTED, "GQA ratio (num_q_heads / num_kv_heads) must be 1, 2, 4 or 8");
+  }
   if (p->head_dim != 256 && p->head_dim != 512)
     return fail(G4_ERR_UNSUPPORTED, "head_dim must be 256 (local) or 512 (global)");
   if (p->window < 0) return fail(G4_ERR_INVALID, "window must be >= 0");

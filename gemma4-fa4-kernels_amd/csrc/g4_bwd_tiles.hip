@@ -75,7 +75,10 @@ struct DkdvCfg {
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 };
 
-template <int D, int DSPLIT, int NKB, bool META>
+// DV / DK select the outputs of a launch: both in one pass, or (when the
+// combined live state does not fit the register file) a dV-only pass (S, P,
+// dV) and a dK-only pass (S, dP, dS, dK).
+template <int D, int DSPLIT, int NKB, bool META, bool DV, bool DK>
 struct DkdvKernel {
   using C = DkdvCfg<D, DSPLIT, NKB>;
   static constexpr int kNB = C::kDH / 32;
@@ -93,13 +96,19 @@ struct DkdvKernel {
   RowReader<C::kCPR> rrd;
   TrReader<C::kCPR> trd;
   TileCopier<C::kCPR, 32, C::kNW> qcp, docp;
-  bf16x8 kf[kNC], vf[kNC];
-  f32x16 dk_acc[kNB], dv_acc[kNB];
+  bf16x8 kf[kNC];
+  bf16x8 vf[DK ? kNC : 1];
+  f32x16 dk_acc[DK ? kNB : 1], dv_acc[DV ? kNB : 1];
 
-  // Step `it` enumerates (query head, query tile) pairs.
+  // Step `it` enumerates (query tile, query head) pairs, query tiles from the
+  // last one down and the GQA group's heads innermost: every workgroup starts
+  // at the top query tile, so concurrently running workgroups of one KV head
+  // stream the same Q / dO tiles at about the same time and share them in L2.
   __device__ __forceinline__ void coords(int it, int& qh, int& i0) const {
-    qh = kvh * grp + it / nqt;
-    i0 = (qt_lo + it % nqt) * C::kBM;
+    // grp is 1, 2, 4 or 8 (validated GQA ratios): shifts, no integer division
+    const int sh = __builtin_ctz(grp);
+    qh = kvh * grp + (it & (grp - 1));
+    i0 = (qt_lo + nqt - 1 - (it >> sh)) * C::kBM;
   }
 
   __device__ __forceinline__ void issue_q(int it, int buf) {
@@ -147,9 +156,29 @@ struct DkdvKernel {
     if constexpr (CP < kNC) {
       bf16x8 qa = rrd.template read<0, 0, CP>(qt);
       sacc = mfma32(qa, kf[CP], sacc);
+      if constexpr (DK) {
+        bf16x8 da = rrd.template read<0, 0, CP>(dot);
+        pacc = mfma32(da, vf[CP], pacc);
+      }
+      sdp_step<CP + 1>(qt, dot, sacc, pacc);
+    }
+  }
+
+  template <int CP>
+  __device__ __forceinline__ void s_only(const char G4_LDS* qt, f32x16& sacc) const {
+    if constexpr (CP < kNC) {
+      bf16x8 qa = rrd.template read<0, 0, CP>(qt);
+      sacc = mfma32(qa, kf[CP], sacc);
+      s_only<CP + 1>(qt, sacc);
+    }
+  }
+
+  template <int CP>
+  __device__ __forceinline__ void dp_only(const char G4_LDS* dot, f32x16& pacc) const {
+    if constexpr (CP < kNC) {
       bf16x8 da = rrd.template read<0, 0, CP>(dot);
       pacc = mfma32(da, vf[CP], pacc);
-      sdp_step<CP + 1>(qt, dot, sacc, pacc);
+      dp_only<CP + 1>(dot, pacc);
     }
   }
 
@@ -165,9 +194,15 @@ struct DkdvKernel {
   __device__ __forceinline__ void step(int cur, int it, int nsteps) {
     int qh, i0;
     coords(it, qh, i0);
-    // Q, dO and the row data of this step have landed (with a single dO
-    // buffer its copies were issued after the previous step's dV phase).
-    vm_wait<0>();
+    // Q and the row data of this step have landed (and dO too when it is
+    // double-buffered); a single dO buffer is refilled after the previous
+    // step's dO reads and waited for just before its first use below.
+    constexpr int kPerQ = decltype(qcp)::kPer;
+    constexpr int kPerDo = decltype(docp)::kPer;
+    if constexpr (C::kDoDouble)
+      vm_wait<0>();
+    else
+      vm_wait<kPerDo>();
     barrier_lds();
     if (it + 1 < nsteps) {
       issue_q(it + 1, cur ^ 1);
@@ -179,17 +214,29 @@ struct DkdvKernel {
 
     __builtin_amdgcn_sched_barrier(0);
     f32x16 sacc = {}, pacc = {};
-    sdp_step<0>(qt, dot, sacc, pacc);
-    mfma_pipeline_hint<2 * kNC, 3, 1>();
+    if constexpr (C::kDoDouble || !DK) {
+      sdp_step<0>(qt, dot, sacc, pacc);
+      mfma_pipeline_hint<(DK ? 2 : 1) * kNC, 3, 1>();
+    } else {
+      s_only<0>(qt, sacc);
+      mfma_pipeline_hint<kNC, 3, 1>();
+      __builtin_amdgcn_sched_barrier(0);
+      // this step's dO copies (older than the Q copies issued above) landed
+      vm_wait<kPerQ>();
+      barrier_lds();
+      __builtin_amdgcn_sched_barrier(0);
+      dp_only<0>(dot, pacc);
+      mfma_pipeline_hint<kNC, 3, 1>();
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (DSPLIT > 1) {
       char G4_LDS* xb = smem + C::kLdsX;
       xchg_write(xb, wave * 2, lane, sacc);
-      xchg_write(xb, wave * 2 + 1, lane, pacc);
+      if constexpr (DK) xchg_write(xb, wave * 2 + 1, lane, pacc);
       barrier_lds();
       xchg_add(xb, (wave ^ 1) * 2, lane, dh, sacc);
-      xchg_add(xb, (wave ^ 1) * 2 + 1, lane, dh, pacc);
+      if constexpr (DK) xchg_add(xb, (wave ^ 1) * 2 + 1, lane, dh, pacc);
     }
 
     // Rows (queries) of the accumulators: 8 (r >> 2) + 4 h32 + (r & 3).
@@ -223,33 +270,41 @@ struct DkdvKernel {
           const bool ok = (i < sq.lq) & (my_j < sq.lk) & in_w & (causal | vis) & doc_ok;
           p = ok ? p : 0.f;
         }
-        const float ds = p * (pacc[r] - del4[e]);
-        pb[r >> 3][r & 7] = (__bf16)p;
-        db[r >> 3][r & 7] = (__bf16)ds;
+        if constexpr (DV) pb[r >> 3][r & 7] = (__bf16)p;
+        if constexpr (DK) db[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - del4[e]));
       }
     }
 
     __builtin_amdgcn_sched_barrier(0);
-    acc_step<0, 0>(dot, pb[0], dv_acc);
-    acc_step<1, 0>(dot, pb[1], dv_acc);
-    mfma_pipeline_hint<2 * kNB, 6, 2>();
+    if constexpr (DV && !DK && !C::kDoDouble) {
+      vm_wait<kPerQ>();
+      barrier_lds();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (DV) {
+      acc_step<0, 0>(dot, pb[0], dv_acc);
+      acc_step<1, 0>(dot, pb[1], dv_acc);
+      mfma_pipeline_hint<2 * kNB, 6, 2>();
+    }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (!C::kDoDouble) {
-      // Single dO buffer: refill once every wave finished its dV reads.
+      // Single dO buffer: refill once every wave finished its dO reads.
       barrier_lds();
       if (it + 1 < nsteps) issue_do(it + 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    acc_step<0, 0>(qt, db[0], dk_acc);
-    acc_step<1, 0>(qt, db[1], dk_acc);
-    mfma_pipeline_hint<2 * kNB, 6, 2>();
+    if constexpr (DK) {
+      acc_step<0, 0>(qt, db[0], dk_acc);
+      acc_step<1, 0>(qt, db[1], dk_acc);
+      mfma_pipeline_hint<2 * kNB, 6, 2>();
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
 };
 
-template <int D, int DSPLIT, int NKB, bool META>
+template <int D, int DSPLIT, int NKB, bool META, bool DV, bool DK>
 __global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a) {
-  using K = DkdvKernel<D, DSPLIT, NKB, META>;
+  using K = DkdvKernel<D, DSPLIT, NKB, META, DV, DK>;
   using C = typename K::C;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   K ker;
@@ -321,7 +376,7 @@ __global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a)
 #pragma unroll
     for (int c = 0; c < K::kNC; ++c) {
       ker.kf[c] = ld_global16(krow + c * 16);
-      ker.vf[c] = ld_global16(vrow + c * 16);
+      if constexpr (DK) ker.vf[c] = ld_global16(vrow + c * 16);
     }
   }
   ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + jc] : -1;
@@ -329,8 +384,8 @@ __global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a)
 
 #pragma unroll
   for (int b = 0; b < K::kNB; ++b) {
-    ker.dk_acc[b] = f32x16{};
-    ker.dv_acc[b] = f32x16{};
+    if constexpr (DK) ker.dk_acc[b] = f32x16{};
+    if constexpr (DV) ker.dv_acc[b] = f32x16{};
   }
 
   if (nsteps > 0) {
@@ -353,12 +408,16 @@ __global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int d = ker.dh * C::kDH + b * 32 + 8 * r4 + 4 * ker.h32;
-        const f32x16& x = ker.dk_acc[b];
-        const f32x16& y = ker.dv_acc[b];
-        *(bf16x4*)(dkrow + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
-                                       (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
-        *(bf16x4*)(dvrow + d) = bf16x4{(__bf16)y[r4 * 4], (__bf16)y[r4 * 4 + 1],
-                                       (__bf16)y[r4 * 4 + 2], (__bf16)y[r4 * 4 + 3]};
+        if constexpr (DK) {
+          const f32x16& x = ker.dk_acc[b];
+          *(bf16x4*)(dkrow + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
+                                         (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
+        }
+        if constexpr (DV) {
+          const f32x16& y = ker.dv_acc[b];
+          *(bf16x4*)(dvrow + d) = bf16x4{(__bf16)y[r4 * 4], (__bf16)y[r4 * 4 + 1],
+                                         (__bf16)y[r4 * 4 + 2], (__bf16)y[r4 * 4 + 3]};
+        }
       }
   }
 }
@@ -683,11 +742,12 @@ hipError_t set_lds(Kern kern, int bytes, bool& done) {
   return e;
 }
 
-template <int D, int DSPLIT, int NKB>
+template <int D, int DSPLIT, int NKB, bool DV, bool DK>
 hipError_t launch_dkdv_cfg(const BwdParams& a, hipStream_t stream) {
   using C = DkdvCfg<D, DSPLIT, NKB>;
   const bool meta = has_meta(a.p);
-  auto kern = meta ? dkdv_kernel<D, DSPLIT, NKB, true> : dkdv_kernel<D, DSPLIT, NKB, false>;
+  auto kern = meta ? dkdv_kernel<D, DSPLIT, NKB, true, DV, DK>
+                   : dkdv_kernel<D, DSPLIT, NKB, false, DV, DK>;
   static bool done[2] = {false, false};
   hipError_t e = set_lds(kern, C::kLdsBytes, done[meta]);
   if (e != hipSuccess) return e;
@@ -719,8 +779,13 @@ hipError_t launch_dq_cfg(const BwdParams& a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_bwd_dkdv(const BwdParams& a, hipStream_t stream) {
-  if (a.p.head_dim == 256) return launch_dkdv_cfg<256, 1, 4>(a, stream);
-  if (a.p.head_dim == 512) return launch_dkdv_cfg<512, 2, 2>(a, stream);
+  if (a.p.head_dim == 256) return launch_dkdv_cfg<256, 1, 4, true, true>(a, stream);
+  if (a.p.head_dim == 512) {
+    // d512: dV and dK in two launches (their combined state exceeds 512 VGPRs)
+    hipError_t e = launch_dkdv_cfg<512, 2, 2, true, false>(a, stream);
+    if (e != hipSuccess) return e;
+    return launch_dkdv_cfg<512, 2, 2, false, true>(a, stream);
+  }
   return hipErrorInvalidValue;
 }
 

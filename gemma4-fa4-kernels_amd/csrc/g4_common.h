@@ -161,38 +161,42 @@ template <int CPR, int BN, int NW>
 struct TileCopier {
   static constexpr int kPer = BN * CPR / (64 * NW);
   static_assert(kPer * 64 * NW == BN * CPR, "tile must split evenly over the waves");
-  uint32_t goff[kPer];  // byte offset of this lane's chunk i
-  int lds_wave;         // byte offset of this wave's first chunk slot
-  __device__ __forceinline__ void init(int64_t row_stride_elems, int wave, int lane) {
+  uint32_t goff[kPer];  // byte offset of this lane's chunk i relative to the tile's first row
+  int wave, lane;
+  int64_t stride_bytes;
+  __device__ __forceinline__ void chunk(int i, int& r, int& c) const {
+    const int p = (i * NW + wave) * 64 + lane;
+    r = p / CPR;
+    c = (p % CPR) ^ (((r & 3) << 2) | ((r >> 2) & 3));
+  }
+  __device__ __forceinline__ void init(int64_t row_stride_elems, int wave_, int lane_) {
+    wave = wave_;
+    lane = lane_;
+    stride_bytes = row_stride_elems * 2;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int p = (i * NW + wave) * 64 + lane;
-      const int r = p / CPR;
-      const int c = (p % CPR) ^ (((r & 3) << 2) | ((r >> 2) & 3));
-      goff[i] = (uint32_t)(r * row_stride_elems * 2 + c * 16);
+      int r, c;
+      chunk(i, r, c);
+      goff[i] = (uint32_t)(r * stride_bytes + c * 16);
     }
-    lds_wave = __builtin_amdgcn_readfirstlane(wave * 64 * 16);
   }
   // rows row0 .. row0 + BN - 1 must all exist.
   __device__ __forceinline__ void issue(const __bf16* tile_row0, char G4_LDS* tile) const {
     const char* g = (const char*)tile_row0;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i)
-      g2l16(g + goff[i], tile + lds_wave + i * NW * 64 * 16);
+    for (int i = 0; i < kPer; ++i) g2l16(g + goff[i], tile + (i * NW + wave) * 64 * 16);
   }
   // Tail tile: rows >= nrows are replaced by row nrows - 1 (their scores are
   // masked, so they only need to be finite data).
-  __device__ __forceinline__ void issue_clamped(const __bf16* tile_row0, int64_t row_stride_elems,
-                                                int nrows, char G4_LDS* tile, int wave,
-                                                int lane) const {
+  __device__ __forceinline__ void issue_clamped(const __bf16* tile_row0, int64_t, int nrows,
+                                                char G4_LDS* tile, int, int) const {
     const char* g = (const char*)tile_row0;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int p = (i * NW + wave) * 64 + lane;
-      const int r = p / CPR;
-      const int c = (p % CPR) ^ (((r & 3) << 2) | ((r >> 2) & 3));
-      const int64_t off = (int64_t)min(r, nrows - 1) * row_stride_elems * 2 + c * 16;
-      g2l16(g + off, tile + lds_wave + i * NW * 64 * 16);
+      int r, c;
+      chunk(i, r, c);
+      g2l16(g + (int64_t)min(r, nrows - 1) * stride_bytes + c * 16,
+            tile + (i * NW + wave) * 64 * 16);
     }
   }
 };
