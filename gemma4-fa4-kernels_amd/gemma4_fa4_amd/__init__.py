@@ -23,6 +23,16 @@ from .model_spec import (
     AttentionLayerSpec,
     Gemma4ModelSpec,
 )
+from .transformers_integration import (
+    BACKEND_NAME,
+    Gemma4DispatchResult,
+    Gemma4MaskPlan,
+    gemma4_fa4_attention_forward,
+    gemma4_fa4_mask,
+    gemma4_fa4_prepared,
+    register_gemma4_fa4_h100,
+    register_gemma4_mi355x,
+)
 
 __all__ = [
     "AttentionLayerSpec",
@@ -40,4 +50,12 @@ __all__ = [
     "GlobalBackwardBudgetExceeded",
     "UnsupportedH100Path",
     "UnsupportedMI355XPath",
+    "BACKEND_NAME",
+    "Gemma4DispatchResult",
+    "Gemma4MaskPlan",
+    "gemma4_fa4_attention_forward",
+    "gemma4_fa4_mask",
+    "gemma4_fa4_prepared",
+    "register_gemma4_fa4_h100",
+    "register_gemma4_mi355x",
 ]
