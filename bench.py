@@ -22,6 +22,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -35,6 +36,7 @@ sys.path.insert(0, os.path.join(ROOT, "gemma4-fa4-kernels_amd"))
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 H100_REF_FWD_BWD_TFLOPS = 121.2  # reference EXP-0035, global d512 S8K fwd+bwd on H100
+CALIBRATION_COPY_BYTES = 256 << 20  # device-to-device copy used to scale HBM counters
 
 
 def pairs_causal(s: int) -> int:
@@ -168,7 +170,45 @@ def kernel_roofline(torch, g, tensors, *, s: int, reps: int):
     }
     per_kernel = {n: round(t, 4) for n, t in times.items()}
     delta_gbs = algo["bwd_delta"][1] / (times["bwd_delta"] * 1e-3) / 1e9
-    return roofline, per_kernel, round(delta_gbs, 1)
+    # Calibration copy of known size: its FETCH_SIZE / WRITE_SIZE counters scale
+    # the dominant kernel's counters to bytes (profiles/traffic.json).
+    src = torch.empty(CALIBRATION_COPY_BYTES, dtype=torch.uint8, device=q.device)
+    dst = torch.empty_like(src)
+    copy_ms = statistics.mean(event_times(torch, lambda: dst.copy_(src), 3, 1))
+    traffic = measured_traffic(dom)
+    if traffic is not None:
+        roofline["traffic"] = traffic["bytes"]
+        roofline["traffic_source"] = traffic["source"]
+    return roofline, per_kernel, round(delta_gbs, 1), round(2 * CALIBRATION_COPY_BYTES / copy_ms / 1e6, 1)
+
+
+def kernel_source_digest() -> str:
+    """SHA-256 over the HIP sources, so recorded counters are tied to the kernels measured."""
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "gemma4-fa4-kernels_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h")):
+            with open(os.path.join(csrc, name), "rb") as f:
+                h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()
+
+
+def measured_traffic(stage: str):
+    """HBM bytes per launch of ``stage`` from profiles/traffic.json, if it matches these sources."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if rec.get("source_digest") != kernel_source_digest() or stage not in rec.get("stages", {}):
+        return None
+    copy = rec["calibration_copy"]
+    fetch_factor = copy["fetch_kib"] * 1024.0 / copy["bytes"]
+    write_factor = copy["write_kib"] * 1024.0 / copy["bytes"]
+    st = rec["stages"][stage]
+    nbytes = st["fetch_kib"] * 1024.0 / fetch_factor + st["write_kib"] * 1024.0 / write_factor
+    return {"bytes": int(nbytes), "source": "profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"}
 
 
 def cpu_baseline(budget_s: float):
@@ -178,7 +218,8 @@ def cpu_baseline(budget_s: float):
     sys.path.insert(0, ROOT)
     from oracle.attention import attention_fwd_bwd
 
-    torch.set_num_threads(os.cpu_count() or 1)
+    # The GPU box grants 16 host threads per GPU whatever os.cpu_count() reports.
+    torch.set_num_threads(max(1, min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", 16)))))
     s, hq, hkv, d = 8192, 32, 4, 512
     q, k, v, do = make_inputs(torch, 1, s, hq, hkv, d, "cpu")
     cu = [0, s]
@@ -235,8 +276,8 @@ def main() -> int:
     s = 8192
     head, tensors = run_case(torch, g, kind="global", s=s, steps=args.steps,
                              warmup=args.warmup, seed=0, dev=dev)
-    roofline, per_kernel, delta_gbs = kernel_roofline(torch, g, tensors, s=s,
-                                                      reps=max(3, args.steps))
+    roofline, per_kernel, delta_gbs, copy_gbs = kernel_roofline(torch, g, tensors, s=s,
+                                                                reps=max(3, args.steps))
     extra = {}
     if not args.no_extra:
         c1, _ = run_case(torch, g, kind="local", s=2048, steps=args.steps, warmup=args.warmup,
@@ -269,6 +310,7 @@ def main() -> int:
         "global_d512_S8192": head,
         "per_kernel_ms": per_kernel,
         "bwd_delta_gbs": delta_gbs,
+        "calibration_copy_gbs": copy_gbs,
         "roofline": roofline,
         **extra,
     }
