@@ -84,9 +84,12 @@ int check_ws(const g4_problem* p, int phase, void* ws, size_t bytes) {
     if (_rc != G4_OK) return _rc; \
   } while (0)
 
-// Workspace: [spans][delta]
+// Workspace: [spans][raise flags][delta]
+int* raise_flags_ptr(const g4_problem& p, void* ws) {
+  return g4::raise_flags_bytes(p) ? (int*)((char*)ws + align256(g4::spans_bytes(p))) : nullptr;
+}
 float* delta_ptr(const g4_problem& p, void* ws) {
-  return (float*)((char*)ws + align256(g4::spans_bytes(p)));
+  return (float*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p));
 }
 
 }  // namespace
@@ -94,6 +97,12 @@ float* delta_ptr(const g4_problem& p, void* ws) {
 namespace g4 {
 size_t delta_bytes(const g4_problem& p) {
   return align256((size_t)q_stream_tokens(p) * p.num_q_heads * 4);
+}
+// One int per (sequence, 32-query group, query head) for the head-dim 512
+// forward's second pass.
+size_t raise_flags_bytes(const g4_problem& p) {
+  if (p.head_dim != 512) return 0;
+  return align256((size_t)p.num_seqs * ((p.seqlen_q + 31) / 32) * p.num_q_heads * 4);
 }
 }  // namespace g4
 
@@ -105,7 +114,7 @@ const char* g4_last_error(void) { return g_last_error.c_str(); }
 
 size_t g4_workspace_bytes(const g4_problem* p, int phase) {
   if (check_problem(p) != G4_OK) return 0;
-  size_t b = align256(g4::spans_bytes(*p));
+  size_t b = align256(g4::spans_bytes(*p)) + g4::raise_flags_bytes(*p);
   if (phase == 1) b += g4::delta_bytes(*p);
   return b;
 }
@@ -138,6 +147,7 @@ int g4_attn_fwd(const g4_problem* p, const void* q, g4_layout ql, const void* k,
     if (e != hipSuccess) return hip_fail(e, "span table");
   }
   g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);
+  a.raise_flags = raise_flags_ptr(*p, ws);
   hipError_t e = g4::launch_fwd(a, st);
   if (e != hipSuccess) return hip_fail(e, "forward");
   return G4_OK;

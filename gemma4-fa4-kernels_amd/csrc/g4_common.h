@@ -201,6 +201,43 @@ struct TileCopier {
   }
 };
 
+// Async copy of a BN-row tile whose rows are exactly 64 16-byte chunks (head
+// dim 512) by NW waves, without per-lane offset tables: chunk i of a lane
+// belongs to the wave-uniform row i * NW + wave, so only the swizzled column
+// (lane ^ swz(row)) is per-lane and is formed at issue time.
+template <int BN, int NW>
+struct RowTileCopier {
+  static constexpr int kPer = BN / NW;
+  static_assert(kPer * NW == BN, "tile must split evenly over the waves");
+  int wave, lane;
+  int64_t stride_bytes;
+  __device__ __forceinline__ void init(int64_t row_stride_elems, int wave_, int lane_) {
+    wave = wave_;
+    lane = lane_;
+    stride_bytes = row_stride_elems * 2;
+  }
+  __device__ __forceinline__ void issue(const __bf16* tile_row0, char G4_LDS* tile) const {
+    const char* g = (const char*)tile_row0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int r = i * NW + wave;
+      const int c = lane ^ (((r & 3) << 2) | ((r >> 2) & 3));
+      g2l16(g + r * stride_bytes + c * 16, tile + r * 64 * 16);
+    }
+  }
+  // Tail tile: rows >= nrows are replaced by row nrows - 1.
+  __device__ __forceinline__ void issue_clamped(const __bf16* tile_row0, int nrows,
+                                                char G4_LDS* tile) const {
+    const char* g = (const char*)tile_row0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int r = i * NW + wave;
+      const int c = lane ^ (((r & 3) << 2) | ((r >> 2) & 3));
+      g2l16(g + (int64_t)min(r, nrows - 1) * stride_bytes + c * 16, tile + r * 64 * 16);
+    }
+  }
+};
+
 // Scheduling hint for a region of N MFMAs fed by LDS reads: PRE reads first,
 // then (1 MFMA, PER reads) repeated, so only a few operand fragments are in
 // flight at any time (the default schedule hoists every read to the top of

@@ -254,7 +254,8 @@ struct FwdKernel {
   }
 };
 
-template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META>
+// FIXUP: rerun only the 32-query groups the wide kernel flagged in raise_flags.
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META, bool FIXUP = false>
 __global__ void __launch_bounds__(NQG * DSPLIT * 64, 1) fwd_kernel(FwdParams a) {
   using K = FwdKernel<D, BN, DSPLIT, NQG, VDOUBLE, META>;
   using C = typename K::C;
@@ -287,6 +288,16 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, 1) fwd_kernel(FwdParams a) 
   const Seq& sq = ker.sq;
   const int i0 = qt * C::kBM;
   if (i0 >= sq.lq) return;
+  if constexpr (FIXUP) {
+    const int nq32 = (p.seqlen_q + 31) / 32;
+    bool need = false;
+#pragma unroll
+    for (int g = 0; g < NQG; ++g) {
+      const int q32 = i0 / 32 + g;
+      if (q32 < nq32) need |= a.raise_flags[((int64_t)s * nq32 + q32) * p.num_q_heads + qh] != 0;
+    }
+    if (!need) return;
+  }
   const int off = sq.lk - sq.lq;  // query i sits at key position i + off
   ker.a0 = i0 + off;
   const int a_last_valid = min(i0 + C::kBM, sq.lq) - 1 + off;
@@ -382,19 +393,326 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, 1) fwd_kernel(FwdParams a) 
   }
 }
 
+// ===========================================================================
+// Software-pipelined forward for wide heads without key metadata.
+//
+// Four waves, one per SIMD, each owning 32 queries and the whole head dim, so
+// no partial scores are exchanged and one K / V tile serves 128 queries.  Per
+// key tile the loop runs two regions:
+//   A: S^T(t+1) = K(t+1) Q^T on MFMA, interleaved with the softmax of tile t
+//      (VALU) and with the async copies of K(t+2) and V(t+1);
+//   B: O^T += V(t)^T P(t)^T on MFMA.
+// One barrier per tile: it publishes K(t+1) and V(t) and retires every read
+// of the buffers refilled in the next region A.
+//
+// The O accumulators (256 AGPRs per lane) are never rescaled.  A row's
+// running maximum m is set by its first admitted tile; later tiles use the
+// same m as long as their maximum stays below m + kRaiseLog2 (log2 units), so
+// P = exp2(s - m) <= 2^kRaiseLog2 is exact in fp32 and in bf16 range and O, l
+// stay far from fp32 overflow.  A row whose scores jump higher (by more than
+// kRaiseLog2 * ln 2 within the row) marks its 32-query group in raise_flags;
+// launch_fwd then reruns exactly those groups with the rescaling kernel.
+// ===========================================================================
+
+constexpr float kRaiseLog2 = 48.0f;
+
+template <int D>
+struct WideCfg {
+  static constexpr int kNW = 4;
+  static constexpr int kNT = kNW * 64;
+  static constexpr int kBM = kNW * 32;
+  static constexpr int kBN = 32;
+  static constexpr int kCPR = D / 8;
+  static constexpr int kTile = kBN * D * 2;
+  static constexpr int kNC = D / 16;  // 16-deep steps of S^T
+  static constexpr int kNB = D / 32;  // 32-wide head-dim blocks of O^T
+  static constexpr int kLdsK = 0;
+  static constexpr int kLdsV = 2 * kTile;
+  static constexpr int kLdsBytes = 4 * kTile;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+};
+
+// Interleave a region of N MFMAs with DS reads, VALU work and VMEM issues.
+template <int N, int DS_PRE, int DS_PER, int VALU_PER, int VMEM_EVERY>
+__device__ __forceinline__ void region_hint() {
+  __builtin_amdgcn_sched_group_barrier(0x100, DS_PRE, 0);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, DS_PER, 0);
+    if constexpr (VALU_PER > 0) __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER, 0);
+    if constexpr (VMEM_EVERY > 0)
+      if (i % VMEM_EVERY == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+  }
+}
+
+template <int D>
+struct FwdWide {
+  using C = WideCfg<D>;
+  static constexpr int kNC = C::kNC;
+  static constexpr int kNB = C::kNB;
+  static constexpr int BN = C::kBN;
+
+  char G4_LDS* smem;
+  Seq sq;
+  int lane, wave, h32;
+  int a0, window, lo_w, hi_c;
+  const __bf16* kbase;
+  const __bf16* vbase;
+  int64_t kstride, vstride;
+  RowReader<C::kCPR> krd;
+  TrReader<C::kCPR> vrd;
+  RowTileCopier<BN, C::kNW> kcp, vcp;
+  bf16x8 qf[kNC];
+  f32x16 o_acc[kNB];
+  float m_run, l_run;
+  bool raise;  // a later tile exceeded this row's maximum by more than kRaiseLog2
+
+  __device__ __forceinline__ void issue_k(int row0, int buf) {
+    char G4_LDS* dst = smem + C::kLdsK + buf * C::kTile;
+    if (row0 + BN <= sq.lk)
+      kcp.issue(kbase + row0 * kstride, dst);
+    else
+      kcp.issue_clamped(kbase + row0 * kstride, sq.lk - row0, dst);
+  }
+  __device__ __forceinline__ void issue_v(int row0, int buf) {
+    char G4_LDS* dst = smem + C::kLdsV + buf * C::kTile;
+    if (row0 + BN <= sq.lk)
+      vcp.issue(vbase + row0 * vstride, dst);
+    else
+      vcp.issue_clamped(vbase + row0 * vstride, sq.lk - row0, dst);
+  }
+
+  template <int CP>
+  __device__ __forceinline__ void s_mma(const char G4_LDS* kt, f32x16& acc) const {
+    if constexpr (CP < kNC) {
+      bf16x8 kfrag = krd.template read<0, 0, CP>(kt);
+      acc = mfma32(kfrag, qf[CP], acc);
+      s_mma<CP + 1>(kt, acc);
+    }
+  }
+
+  template <int HK, int B>
+  __device__ __forceinline__ void pv_mma(const char G4_LDS* vt, const bf16x8& pb) {
+    if constexpr (B < kNB) {
+      bf16x8 vfrag = vrd.template read<16 * HK, 0, B>(vt);
+      o_acc[B] = mfma32(vfrag, pb, o_acc[B]);
+      pv_mma<HK, B + 1>(vt, pb);
+    }
+  }
+
+  // Softmax of one tile's raw scores (keys kb0 + ...) into bf16 P.
+  __device__ __forceinline__ void softmax(f32x16& s, int kb0, bf16x8 (&pb)[2]) {
+    const bool full = (kb0 + BN <= sq.lk) && (kb0 + BN - 1 <= a0) &&
+                      (window <= 0 || kb0 > a0 + C::kBM - 1 - window);
+    if (!full) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int j = kb0 + 8 * (r >> 2) + 4 * h32 + (r & 3);
+        const bool ok = (j >= lo_w) & (j <= hi_c);
+        s[r] = ok ? s[r] : kNegInf;
+      }
+    }
+    float mx = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+    mx = fmaxf(mx, wave_xor32(mx)) * kLog2e;
+    if (m_run == kNegInf) m_run = mx;  // first admitted tile of the row (or still none)
+    raise |= mx > m_run + kRaiseLog2;
+    const float m_use = m_run == kNegInf ? 0.f : m_run;
+    float rs = 0.f;
+#pragma unroll
+    for (int hk = 0; hk < 2; ++hk)
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const float pv = fast_exp2(__builtin_fmaf(s[hk * 8 + m], kLog2e, -m_use));
+        rs += pv;
+        pb[hk][m] = (__bf16)pv;
+      }
+    l_run += rs;
+  }
+};
+
+template <int D>
+__global__ void __launch_bounds__(256, 1) fwd_wide_kernel(FwdParams a) {
+  using K = FwdWide<D>;
+  using C = typename K::C;
+  constexpr int BN = C::kBN;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  K ker;
+  ker.smem = (char G4_LDS*)smem_raw;
+  const g4_problem& p = a.p;
+  const int tid = threadIdx.x;
+  ker.lane = tid & 63;
+  ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  ker.h32 = ker.lane >> 5;
+  const int l32 = ker.lane & 31;
+
+  const int grp = p.num_q_heads / p.num_kv_heads;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_kvh = a.num_seqs * a.ntq * grp;
+  const int kvh = L / per_kvh;
+  const int rem = L % per_kvh;
+  const int rank = rem / grp;
+  const int qh = kvh * grp + rem % grp;
+  const int s = rank / a.ntq;
+  const int qt = zigzag(rank % a.ntq, a.ntq);
+
+  ker.sq = resolve_seq(p, s);
+  const Seq& sq = ker.sq;
+  const int i0 = qt * C::kBM;
+  if (i0 >= sq.lq) return;
+  const int off = sq.lk - sq.lq;
+  ker.a0 = i0 + off;
+  const int a_last_valid = min(i0 + C::kBM, sq.lq) - 1 + off;
+  ker.window = p.window;
+
+  int klo, khi;
+  query_tile_key_range(ker.a0, a_last_valid, sq.lk, p.window, -1, klo, khi);
+  const int t_first = klo / BN;
+  const int ntiles = (khi + BN - 1) / BN - t_first;
+
+  ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
+  ker.vbase = a.v + tok_off(sq, s, sq.ktok, 0, a.vl) + (int64_t)kvh * a.vl.head_stride;
+  ker.kstride = a.kl.token_stride;
+  ker.vstride = a.vl.token_stride;
+  ker.krd.init(ker.lane, 0);
+  ker.vrd.init(ker.lane, 0);
+  ker.kcp.init(ker.kstride, ker.wave, ker.lane);
+  ker.vcp.init(ker.vstride, ker.wave, ker.lane);
+
+  const int my_i = i0 + ker.wave * 32 + l32;
+  const int my_a = my_i + off;
+  const bool q_valid = my_i < sq.lq;
+  ker.lo_w = p.window > 0 ? my_a - p.window + 1 : -0x40000000;
+  ker.hi_c = min(my_a, sq.lk - 1);
+  {
+    const __bf16* qrow = a.q + tok_off(sq, s, sq.qtok, min(my_i, sq.lq - 1), a.ql) +
+                         (int64_t)qh * a.ql.head_stride + ker.h32 * 8;
+#pragma unroll
+    for (int c = 0; c < K::kNC; ++c) {
+      bf16x8 x = ld_global16(qrow + c * 16);
+      ker.qf[c] = q_valid ? x : bf16x8{};
+    }
+  }
+  ker.m_run = kNegInf;
+  ker.l_run = 0.f;
+  ker.raise = false;
+#pragma unroll
+  for (int b = 0; b < K::kNB; ++b) ker.o_acc[b] = f32x16{};
+
+  f32x16 s_cur = {};
+  if (ntiles > 0) {
+    // Prologue: K(0), V(0), K(1); S(0).
+    ker.issue_k(t_first * BN, 0);
+    ker.issue_v(t_first * BN, 0);
+    if (ntiles > 1) {
+      ker.issue_k((t_first + 1) * BN, 1);
+      vm_wait<decltype(ker.kcp)::kPer>();
+    } else {
+      vm_wait<0>();
+    }
+    barrier_lds();
+    __builtin_amdgcn_sched_barrier(0);
+    ker.template s_mma<0>(ker.smem + C::kLdsK, s_cur);
+    mfma_pipeline_hint<K::kNC, 3, 1>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    const int cur = it & 1, nxt = cur ^ 1;
+    const int kb0 = (t_first + it) * BN;
+    // K(it + 1) and V(it) have landed in every wave; every wave is done with
+    // the K buffer of tile it and the V buffer of tile it - 1.
+    vm_wait<0>();
+    barrier_lds();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- region A: S(it + 1) || softmax(it) || copies K(it + 2), V(it + 1)
+    if (it + 2 < ntiles) ker.issue_k(kb0 + 2 * BN, cur);
+    if (it + 1 < ntiles) ker.issue_v(kb0 + BN, nxt);
+    f32x16 s_nxt = {};
+    bf16x8 pb[2];
+    if (it + 1 < ntiles) {
+      ker.template s_mma<0>(ker.smem + C::kLdsK + nxt * C::kTile, s_nxt);
+      ker.softmax(s_cur, kb0, pb);
+      region_hint<K::kNC, 3, 1, 4, 2>();
+    } else {
+      ker.softmax(s_cur, kb0, pb);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- region B: O^T += V(it)^T P(it)^T
+    const char G4_LDS* vt = ker.smem + C::kLdsV + cur * C::kTile;
+    ker.template pv_mma<0, 0>(vt, pb[0]);
+    ker.template pv_mma<1, 0>(vt, pb[1]);
+    mfma_pipeline_hint<2 * K::kNB, 6, 2>();
+    __builtin_amdgcn_sched_barrier(0);
+    s_cur = s_nxt;
+  }
+
+  // Every 32-query group reports whether its rows need the rescaling pass.
+  const int q32 = i0 / 32 + ker.wave;
+  const int nq32 = (p.seqlen_q + 31) / 32;
+  const bool raise_any = __ballot(ker.raise && q_valid) != 0;
+  if (ker.lane == 0 && q32 < nq32)
+    a.raise_flags[((int64_t)s * nq32 + q32) * p.num_q_heads + qh] = raise_any ? 1 : 0;
+
+  const float l_tot = ker.l_run + wave_xor32(ker.l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (q_valid) {
+    __bf16* orow = a.o + tok_off(sq, s, sq.qtok, my_i, a.ol) + (int64_t)qh * a.ol.head_stride;
+#pragma unroll
+    for (int b = 0; b < K::kNB; ++b) {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = b * 32 + 8 * r4 + 4 * ker.h32;
+        const f32x16& acc = ker.o_acc[b];
+        bf16x4 v = {(__bf16)(acc[r4 * 4] * inv), (__bf16)(acc[r4 * 4 + 1] * inv),
+                    (__bf16)(acc[r4 * 4 + 2] * inv), (__bf16)(acc[r4 * 4 + 3] * inv)};
+        *(bf16x4*)(orow + d) = v;
+      }
+    }
+    if (ker.h32 == 0) {
+      a.lse[lse_off(p, sq, s, qh, my_i)] =
+          l_tot > 0.f ? (ker.m_run + fast_log2(l_tot)) * kLn2 : kNegInf;
+    }
+  }
+}
+
+template <int D>
+static hipError_t launch_fwd_wide(const FwdParams& a, hipStream_t stream) {
+  using C = WideCfg<D>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)fwd_wide_kernel<D>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  FwdParams b = a;
+  b.ntq = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
+  const int64_t nblocks = (int64_t)b.num_seqs * b.ntq * a.p.num_q_heads;
+  if (nblocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fwd_wide_kernel<D>, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes,
+                     stream, b);
+  return hipGetLastError();
+}
+
 template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE>
-static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream) {
+static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fixup = false) {
   using C = FwdCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
   const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
                     a.p.document_ids != nullptr;
-  auto kern = meta ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, true>
-                   : fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false>;
-  static bool attr_set[2] = {false, false};
-  if (!attr_set[meta]) {
+  auto kern = meta    ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, true>
+              : fixup ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false, true>
+                      : fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false>;
+  const int variant = meta ? 1 : fixup ? 2 : 0;
+  static bool attr_set[3] = {false, false, false};
+  if (!attr_set[variant]) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
     if (e != hipSuccess) return e;
-    attr_set[meta] = true;
+    attr_set[variant] = true;
   }
   FwdParams b = a;
   b.ntq = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
@@ -406,7 +724,15 @@ static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream) {
 
 hipError_t launch_fwd(const FwdParams& a, hipStream_t stream) {
   if (a.p.head_dim == 256) return launch_fwd_cfg<256, 64, 1, 4, true>(a, stream);
-  if (a.p.head_dim == 512) return launch_fwd_cfg<512, 32, 2, 2, true>(a, stream);
+  if (a.p.head_dim == 512) {
+    const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
+                      a.p.document_ids != nullptr;
+    if (meta || a.raise_flags == nullptr) return launch_fwd_cfg<512, 32, 2, 2, true>(a, stream);
+    // Fast pass, then the rescaling kernel on the 32-query groups it flagged.
+    hipError_t e = launch_fwd_wide<512>(a, stream);
+    if (e != hipSuccess) return e;
+    return launch_fwd_cfg<512, 32, 2, 2, true>(a, stream, /*fixup=*/true);
+  }
   return hipErrorInvalidValue;
 }
 

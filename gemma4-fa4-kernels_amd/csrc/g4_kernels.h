@@ -17,6 +17,7 @@ struct FwdParams {
   const int* span_hi;  // per K-stream token: last position of its vision span (or itself)
   int num_seqs;
   int ntq;             // query tiles per sequence (set by the launcher)
+  int* raise_flags;    // per (seq, 32-query group, head): rows the fast pass cannot finish
 };
 
 struct BwdParams {
@@ -42,6 +43,7 @@ struct BwdParams {
 // Workspace layout helpers (bytes).
 size_t spans_bytes(const g4_problem& p);
 size_t delta_bytes(const g4_problem& p);
+size_t raise_flags_bytes(const g4_problem& p);
 int64_t k_stream_tokens(const g4_problem& p);
 int64_t q_stream_tokens(const g4_problem& p);
 
