@@ -74,7 +74,14 @@ __device__ __forceinline__ bf16x8 ld_global16(const void* p) {
   return *(const bf16x8*)p;
 }
 
-__device__ __forceinline__ float wave_xor32(float x) { return __shfl_xor(x, 32, 64); }
+// Value of lane l ^ 32.  v_permlane32_swap_b32 with both operands x returns
+// (x with lanes 32-63 replaced by lanes 0-31, x with lanes 0-31 replaced by
+// lanes 32-63): a VALU exchange, so no LDS permute and no LDS-counter wait
+// that would drain the wave's in-flight operand reads.
+__device__ __forceinline__ float wave_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
 
 // Workgroup barrier that orders LDS traffic only.  Unlike __syncthreads() it
 // does not drain outstanding global loads, so tile copies issued earlier stay

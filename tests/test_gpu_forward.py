@@ -121,3 +121,51 @@ def test_forward_is_bitwise_repeatable_on_a_side_stream():
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def _raise_flags(st, nseg, max_q):
+    """The d512 forward's per-(segment, 32-query group, head) raise flags (workspace head)."""
+    n = nseg * ((max_q + 31) // 32) * 32
+    return st.ws[: 4 * n].view(torch.int32).cpu()
+
+
+@pytest.mark.parametrize("lq,lk", [([300, 450], [300, 450]), ([130], [700])])
+def test_global_rescaling_pass_for_large_score_jumps(lq, lk):
+    # Tiny first keys, then N(0, 1) keys against N(0, 1) queries: later tiles'
+    # row maxima exceed the first tile's by far more than 2^48 in exp2 terms,
+    # so the fast pass flags those rows and the rescaling pass recomputes them.
+    from gemma4_fa4_amd import ops
+    from gemma4_fa4_amd.attention import _packed_plan
+
+    g = _g()
+    q, k, v, _, _ = qkv(900 + sum(lq), sum(lq), sum(lk), 32, 4, 512, unit_logits=False)
+    starts = cu(lk)[:-1].tolist()
+    for s0 in starts:
+        k[s0:s0 + 40] = (k[s0:s0 + 40].float() / 64).to(torch.bfloat16)
+    cq, ck = cu(lq), cu(lk)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    plan = _packed_plan(qd, kd, cq.to(DEV), ck.to(DEV), max(lq), max(lk), g.GLOBAL_ATTENTION)
+    st = ops.Stages(plan, qd, kd, vd, torch.zeros_like(qd))
+    st.forward()
+    torch.cuda.synchronize()
+    assert int(_raise_flags(st, len(lq), max(lq)).sum()) > 0, "no row took the rescaling pass"
+    o_ref, l_ref, *_ = oracle_fwd_bwd(q, k, v, cq, ck, window=None)
+    check_forward(st.o, st.lse, o_ref, l_ref, local=False, label=f"global rescale {lq}/{lk}")
+    o2, lse2 = g.fa4_global_varlen_forward_only(qd, kd, vd, cq.to(DEV), ck.to(DEV),
+                                                max_seqlen_q=max(lq), max_seqlen_k=max(lk))
+    assert torch.equal(o2, st.o) and torch.equal(lse2, st.lse)
+
+
+def test_global_unit_logits_need_no_rescaling_pass():
+    from gemma4_fa4_amd import ops
+    from gemma4_fa4_amd.attention import _packed_plan
+
+    g = _g()
+    s = 1000
+    q, k, v, _, _ = qkv(77, s, s, 32, 4, 512)
+    c = cu([s]).to(DEV)
+    st = ops.Stages(_packed_plan(q.to(DEV), k.to(DEV), c, c, s, s, g.GLOBAL_ATTENTION),
+                    q.to(DEV), k.to(DEV), v.to(DEV), torch.zeros_like(q).to(DEV))
+    st.forward()
+    torch.cuda.synchronize()
+    assert int(_raise_flags(st, 1, s).sum()) == 0
