@@ -19,6 +19,8 @@
 //
 // With DSPLIT = 2 (head dim 512) the two waves of a pair own the two halves of
 // the head dimension and exchange their partial S / dP through LDS.
+#include <type_traits>
+
 #include "g4_kernels.h"
 
 namespace g4 {
@@ -54,7 +56,7 @@ __device__ __forceinline__ void xchg_add(const char G4_LDS* xb, int slot, int la
 // dK / dV
 // ===========================================================================
 
-template <int D, int DSPLIT, int NKB>
+template <int D, int DSPLIT, int NKB, bool DV, bool DK>
 struct DkdvCfg {
   static constexpr int kNW = NKB * DSPLIT;
   static constexpr int kNT = kNW * 64;
@@ -63,8 +65,15 @@ struct DkdvCfg {
   static constexpr int kDH = D / DSPLIT;
   static constexpr int kCPR = D / 8;
   static constexpr int kTile = kBM * D * 2;  // Q or dO tile bytes
-  static constexpr bool kDoDouble = DSPLIT == 1;
-  static constexpr int kXBytes = DSPLIT > 1 ? kNW * 2 * 4096 : 0;
+  // Partial score tiles each wave of a head-dim pair exports: S, and dP when
+  // the launch computes dK.
+  static constexpr int kXPer = DSPLIT > 1 ? (DK ? 2 : 1) : 0;
+  static constexpr int kXBytes = kNW * kXPer * 4096;
+  // dO is double-buffered unless the pair exchange of S and dP needs its
+  // room; single-buffered, it is refilled as soon as the exchange barrier
+  // retires the dP reads (dK-only launches never read it again).
+  static constexpr bool kDoDouble = DSPLIT == 1 || !DK;
+  static_assert(kDoDouble || !DV, "single-buffered dO is refilled before dV would read it");
   static constexpr int kLdsQ = 0;
   static constexpr int kLdsDo = kLdsQ + 2 * kTile;
   static constexpr int kLdsX = kLdsDo + (kDoDouble ? 2 : 1) * kTile;
@@ -80,7 +89,7 @@ struct DkdvCfg {
 // dV) and a dK-only pass (S, dP, dS, dK).
 template <int D, int DSPLIT, int NKB, bool META, bool DV, bool DK>
 struct DkdvKernel {
-  using C = DkdvCfg<D, DSPLIT, NKB>;
+  using C = DkdvCfg<D, DSPLIT, NKB, DV, DK>;
   static constexpr int kNB = C::kDH / 32;
   static constexpr int kNC = C::kDH / 16;
 
@@ -95,7 +104,11 @@ struct DkdvKernel {
   int64_t tq;
   RowReader<C::kCPR> rrd;
   TrReader<C::kCPR> trd;
-  TileCopier<C::kCPR, 32, C::kNW> qcp, docp;
+  // 64-chunk rows (head dim 512): the copy row is wave-uniform, so no
+  // per-lane offset tables are needed.
+  using Copier = std::conditional_t<C::kCPR == 64, RowTileCopier<32, C::kNW>,
+                                    TileCopier<C::kCPR, 32, C::kNW>>;
+  Copier qcp, docp;
   bf16x8 kf[kNC];
   bf16x8 vf[DK ? kNC : 1];
   f32x16 dk_acc[DK ? kNB : 1], dv_acc[DV ? kNB : 1];
@@ -164,24 +177,6 @@ struct DkdvKernel {
     }
   }
 
-  template <int CP>
-  __device__ __forceinline__ void s_only(const char G4_LDS* qt, f32x16& sacc) const {
-    if constexpr (CP < kNC) {
-      bf16x8 qa = rrd.template read<0, 0, CP>(qt);
-      sacc = mfma32(qa, kf[CP], sacc);
-      s_only<CP + 1>(qt, sacc);
-    }
-  }
-
-  template <int CP>
-  __device__ __forceinline__ void dp_only(const char G4_LDS* dot, f32x16& pacc) const {
-    if constexpr (CP < kNC) {
-      bf16x8 da = rrd.template read<0, 0, CP>(dot);
-      pacc = mfma32(da, vf[CP], pacc);
-      dp_only<CP + 1>(dot, pacc);
-    }
-  }
-
   template <int M, int B>
   __device__ __forceinline__ void acc_step(const char G4_LDS* t, const bf16x8& b, f32x16* acc) const {
     if constexpr (B < kNB) {
@@ -194,15 +189,9 @@ struct DkdvKernel {
   __device__ __forceinline__ void step(int cur, int it, int nsteps) {
     int qh, i0;
     coords(it, qh, i0);
-    // Q and the row data of this step have landed (and dO too when it is
-    // double-buffered); a single dO buffer is refilled after the previous
-    // step's dO reads and waited for just before its first use below.
-    constexpr int kPerQ = decltype(qcp)::kPer;
-    constexpr int kPerDo = decltype(docp)::kPer;
-    if constexpr (C::kDoDouble)
-      vm_wait<0>();
-    else
-      vm_wait<kPerDo>();
+    // Every copy for this step (Q, row data, dO) has landed in every wave;
+    // every wave is done with the buffers refilled below.
+    vm_wait<0>();
     barrier_lds();
     if (it + 1 < nsteps) {
       issue_q(it + 1, cur ^ 1);
@@ -214,29 +203,20 @@ struct DkdvKernel {
 
     __builtin_amdgcn_sched_barrier(0);
     f32x16 sacc = {}, pacc = {};
-    if constexpr (C::kDoDouble || !DK) {
-      sdp_step<0>(qt, dot, sacc, pacc);
-      mfma_pipeline_hint<(DK ? 2 : 1) * kNC, 3, 1>();
-    } else {
-      s_only<0>(qt, sacc);
-      mfma_pipeline_hint<kNC, 3, 1>();
-      __builtin_amdgcn_sched_barrier(0);
-      // this step's dO copies (older than the Q copies issued above) landed
-      vm_wait<kPerQ>();
-      barrier_lds();
-      __builtin_amdgcn_sched_barrier(0);
-      dp_only<0>(dot, pacc);
-      mfma_pipeline_hint<kNC, 3, 1>();
-    }
+    sdp_step<0>(qt, dot, sacc, pacc);
+    mfma_pipeline_hint<(DK ? 2 : 1) * kNC, 3, 1>();
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (DSPLIT > 1) {
       char G4_LDS* xb = smem + C::kLdsX;
-      xchg_write(xb, wave * 2, lane, sacc);
-      if constexpr (DK) xchg_write(xb, wave * 2 + 1, lane, pacc);
+      xchg_write(xb, wave * C::kXPer, lane, sacc);
+      if constexpr (DK) xchg_write(xb, wave * C::kXPer + 1, lane, pacc);
       barrier_lds();
-      xchg_add(xb, (wave ^ 1) * 2, lane, dh, sacc);
-      if constexpr (DK) xchg_add(xb, (wave ^ 1) * 2 + 1, lane, dh, pacc);
+      // Single dO buffer: every wave's dP reads are retired; refill it now.
+      if constexpr (!C::kDoDouble)
+        if (it + 1 < nsteps) issue_do(it + 1, 0);
+      xchg_add(xb, (wave ^ 1) * C::kXPer, lane, dh, sacc);
+      if constexpr (DK) xchg_add(xb, (wave ^ 1) * C::kXPer + 1, lane, dh, pacc);
     }
 
     // Rows (queries) of the accumulators: 8 (r >> 2) + 4 h32 + (r & 3).
@@ -276,21 +256,10 @@ struct DkdvKernel {
     }
 
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (DV && !DK && !C::kDoDouble) {
-      vm_wait<kPerQ>();
-      barrier_lds();
-    }
-    __builtin_amdgcn_sched_barrier(0);
     if constexpr (DV) {
       acc_step<0, 0>(dot, pb[0], dv_acc);
       acc_step<1, 0>(dot, pb[1], dv_acc);
       mfma_pipeline_hint<2 * kNB, 6, 2>();
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (!C::kDoDouble) {
-      // Single dO buffer: refill once every wave finished its dO reads.
-      barrier_lds();
-      if (it + 1 < nsteps) issue_do(it + 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (DK) {
@@ -744,7 +713,7 @@ hipError_t set_lds(Kern kern, int bytes, bool& done) {
 
 template <int D, int DSPLIT, int NKB, bool DV, bool DK>
 hipError_t launch_dkdv_cfg(const BwdParams& a, hipStream_t stream) {
-  using C = DkdvCfg<D, DSPLIT, NKB>;
+  using C = DkdvCfg<D, DSPLIT, NKB, DV, DK>;
   const bool meta = has_meta(a.p);
   auto kern = meta ? dkdv_kernel<D, DSPLIT, NKB, true, DV, DK>
                    : dkdv_kernel<D, DSPLIT, NKB, false, DV, DK>;

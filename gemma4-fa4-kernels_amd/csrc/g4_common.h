@@ -232,9 +232,10 @@ struct RowTileCopier {
       g2l16(g + r * stride_bytes + c * 16, tile + r * 64 * 16);
     }
   }
-  // Tail tile: rows >= nrows are replaced by row nrows - 1.
-  __device__ __forceinline__ void issue_clamped(const __bf16* tile_row0, int nrows,
-                                                char G4_LDS* tile) const {
+  // Tail tile: rows >= nrows are replaced by row nrows - 1.  (The trailing
+  // arguments match TileCopier::issue_clamped.)
+  __device__ __forceinline__ void issue_clamped(const __bf16* tile_row0, int64_t, int nrows,
+                                                char G4_LDS* tile, int = 0, int = 0) const {
     const char* g = (const char*)tile_row0;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {

@@ -473,14 +473,14 @@ struct FwdWide {
     if (row0 + BN <= sq.lk)
       kcp.issue(kbase + row0 * kstride, dst);
     else
-      kcp.issue_clamped(kbase + row0 * kstride, sq.lk - row0, dst);
+      kcp.issue_clamped(kbase + row0 * kstride, kstride, sq.lk - row0, dst);
   }
   __device__ __forceinline__ void issue_v(int row0, int buf) {
     char G4_LDS* dst = smem + C::kLdsV + buf * C::kTile;
     if (row0 + BN <= sq.lk)
       vcp.issue(vbase + row0 * vstride, dst);
     else
-      vcp.issue_clamped(vbase + row0 * vstride, sq.lk - row0, dst);
+      vcp.issue_clamped(vbase + row0 * vstride, vstride, sq.lk - row0, dst);
   }
 
   template <int CP>
