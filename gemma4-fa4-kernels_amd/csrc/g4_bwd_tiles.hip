@@ -56,26 +56,27 @@ __device__ __forceinline__ void xchg_add(const char G4_LDS* xb, int slot, int la
 // dK / dV
 // ===========================================================================
 
-template <int D, int DSPLIT, int NKB, bool DV, bool DK>
+template <int D, int DSPLIT, int NKB, bool DV, bool DK, int KPW>
 struct DkdvCfg {
   static constexpr int kNW = NKB * DSPLIT;
   static constexpr int kNT = kNW * 64;
-  static constexpr int kBN = NKB * 32;  // keys per workgroup
-  static constexpr int kBM = 32;        // queries per step
+  static constexpr int kBN = NKB * KPW * 32;  // keys per workgroup
+  static constexpr int kBM = 32;              // queries per step
   static constexpr int kDH = D / DSPLIT;
   static constexpr int kCPR = D / 8;
   static constexpr int kTile = kBM * D * 2;  // Q or dO tile bytes
-  // Partial score tiles each wave of a head-dim pair exports: S, and dP when
-  // the launch computes dK.
+  // Partial score tiles each wave of a head-dim pair exports per key block:
+  // S, and dP when the launch computes dK.
   static constexpr int kXPer = DSPLIT > 1 ? (DK ? 2 : 1) : 0;
-  static constexpr int kXBytes = kNW * kXPer * 4096;
-  // dO is double-buffered unless the pair exchange of S and dP needs its
-  // room; single-buffered, it is refilled as soon as the exchange barrier
-  // retires the dP reads (dK-only launches never read it again).
-  static constexpr bool kDoDouble = DSPLIT == 1 || !DK;
-  static_assert(kDoDouble || !DV, "single-buffered dO is refilled before dV would read it");
+  static constexpr int kXBytes = kNW * KPW * kXPer * 4096;
+  // With a head-dim pair exchange, a tile no MFMA reads after the exchange
+  // (Q without dK, dO without dV) is single-buffered and refilled as soon as
+  // the exchange barrier retires its reads; otherwise tiles are double-buffered
+  // and refilled at the top of the step.
+  static constexpr bool kQDouble = DSPLIT == 1 || DK;
+  static constexpr bool kDoDouble = DSPLIT == 1 || DV;
   static constexpr int kLdsQ = 0;
-  static constexpr int kLdsDo = kLdsQ + 2 * kTile;
+  static constexpr int kLdsDo = kLdsQ + (kQDouble ? 2 : 1) * kTile;
   static constexpr int kLdsX = kLdsDo + (kDoDouble ? 2 : 1) * kTile;
   static constexpr int kLdsLd = kLdsX + kXBytes;    // [buf][lse x 32 | delta x 32] fp32
   static constexpr int kLdsMeta = kLdsLd + 2 * 256;  // [buf][vid x 32 | doc x 32] int32
@@ -87,9 +88,11 @@ struct DkdvCfg {
 // DV / DK select the outputs of a launch: both in one pass, or (when the
 // combined live state does not fit the register file) a dV-only pass (S, P,
 // dV) and a dK-only pass (S, dP, dS, dK).
-template <int D, int DSPLIT, int NKB, bool META, bool DV, bool DK>
+// KPW key blocks of 32 per wave: each Q / dO fragment read from LDS feeds KPW
+// MFMAs (one per key block), at KPW times the accumulator registers.
+template <int D, int DSPLIT, int NKB, bool META, bool DV, bool DK, int KPW>
 struct DkdvKernel {
-  using C = DkdvCfg<D, DSPLIT, NKB, DV, DK>;
+  using C = DkdvCfg<D, DSPLIT, NKB, DV, DK, KPW>;
   static constexpr int kNB = C::kDH / 32;
   static constexpr int kNC = C::kDH / 16;
 
@@ -97,9 +100,10 @@ struct DkdvKernel {
   const BwdParams* a;
   Seq sq;
   int s, lane, wave, dh, h32, kb;
-  int off, j0, my_j;
+  int off, j0;
+  int my_j[KPW];
   bool has_vid, has_doc, has_meta;
-  int my_vid, my_doc;
+  int my_vid[KPW], my_doc[KPW];
   int grp, kvh, qt_lo, nqt;
   int64_t tq;
   RowReader<C::kCPR> rrd;
@@ -109,9 +113,9 @@ struct DkdvKernel {
   using Copier = std::conditional_t<C::kCPR == 64, RowTileCopier<32, C::kNW>,
                                     TileCopier<C::kCPR, 32, C::kNW>>;
   Copier qcp, docp;
-  bf16x8 kf[kNC];
-  bf16x8 vf[DK ? kNC : 1];
-  f32x16 dk_acc[DK ? kNB : 1], dv_acc[DV ? kNB : 1];
+  bf16x8 kf[KPW][kNC];
+  bf16x8 vf[KPW][DK ? kNC : 1];
+  f32x16 dk_acc[KPW][DK ? kNB : 1], dv_acc[KPW][DV ? kNB : 1];
 
   // Step `it` enumerates (query tile, query head) pairs, query tiles from the
   // last one down and the GQA group's heads innermost: every workgroup starts
@@ -128,7 +132,7 @@ struct DkdvKernel {
     int qh, i0;
     coords(it, qh, i0);
     const __bf16* base = a->q + tok_off(sq, s, sq.qtok, i0, a->ql) + (int64_t)qh * a->ql.head_stride;
-    char G4_LDS* dst = smem + C::kLdsQ + buf * C::kTile;
+    char G4_LDS* dst = smem + C::kLdsQ + (C::kQDouble ? buf : 0) * C::kTile;
     if (i0 + C::kBM <= sq.lq)
       qcp.issue(base, dst);
     else
@@ -139,7 +143,7 @@ struct DkdvKernel {
     coords(it, qh, i0);
     const __bf16* base =
         a->dout + tok_off(sq, s, sq.qtok, i0, a->dol) + (int64_t)qh * a->dol.head_stride;
-    char G4_LDS* dst = smem + C::kLdsDo + buf * C::kTile;
+    char G4_LDS* dst = smem + C::kLdsDo + (C::kDoDouble ? buf : 0) * C::kTile;
     if (i0 + C::kBM <= sq.lq)
       docp.issue(base, dst);
     else
@@ -165,23 +169,27 @@ struct DkdvKernel {
 
   template <int CP>
   __device__ __forceinline__ void sdp_step(const char G4_LDS* qt, const char G4_LDS* dot,
-                                           f32x16& sacc, f32x16& pacc) const {
+                                           f32x16 (&sacc)[KPW], f32x16 (&pacc)[KPW]) const {
     if constexpr (CP < kNC) {
       bf16x8 qa = rrd.template read<0, 0, CP>(qt);
-      sacc = mfma32(qa, kf[CP], sacc);
+#pragma unroll
+      for (int kp = 0; kp < KPW; ++kp) sacc[kp] = mfma32(qa, kf[kp][CP], sacc[kp]);
       if constexpr (DK) {
         bf16x8 da = rrd.template read<0, 0, CP>(dot);
-        pacc = mfma32(da, vf[CP], pacc);
+#pragma unroll
+        for (int kp = 0; kp < KPW; ++kp) pacc[kp] = mfma32(da, vf[kp][CP], pacc[kp]);
       }
       sdp_step<CP + 1>(qt, dot, sacc, pacc);
     }
   }
 
   template <int M, int B>
-  __device__ __forceinline__ void acc_step(const char G4_LDS* t, const bf16x8& b, f32x16* acc) const {
+  __device__ __forceinline__ void acc_step(const char G4_LDS* t, const bf16x8 (&b)[KPW][2],
+                                           f32x16 (&acc)[KPW][kNB]) const {
     if constexpr (B < kNB) {
       bf16x8 x = trd.template read<16 * M, 0, B>(t);
-      acc[B] = mfma32(x, b, acc[B]);
+#pragma unroll
+      for (int kp = 0; kp < KPW; ++kp) acc[kp][B] = mfma32(x, b[kp][M], acc[kp][B]);
       acc_step<M, B + 1>(t, b, acc);
     }
   }
@@ -194,29 +202,39 @@ struct DkdvKernel {
     vm_wait<0>();
     barrier_lds();
     if (it + 1 < nsteps) {
-      issue_q(it + 1, cur ^ 1);
+      if constexpr (C::kQDouble) issue_q(it + 1, cur ^ 1);
       issue_rows(it + 1, cur ^ 1);
       if constexpr (C::kDoDouble) issue_do(it + 1, cur ^ 1);
     }
-    const char G4_LDS* qt = smem + C::kLdsQ + cur * C::kTile;
+    const char G4_LDS* qt = smem + C::kLdsQ + (C::kQDouble ? cur : 0) * C::kTile;
     const char G4_LDS* dot = smem + C::kLdsDo + (C::kDoDouble ? cur : 0) * C::kTile;
 
     __builtin_amdgcn_sched_barrier(0);
-    f32x16 sacc = {}, pacc = {};
+    f32x16 sacc[KPW], pacc[KPW];
+#pragma unroll
+    for (int kp = 0; kp < KPW; ++kp) sacc[kp] = pacc[kp] = f32x16{};
     sdp_step<0>(qt, dot, sacc, pacc);
-    mfma_pipeline_hint<(DK ? 2 : 1) * kNC, 3, 1>();
+    mfma_read_hint<(DK ? 2 : 1) * kNC, KPW, 1, 3>();
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (DSPLIT > 1) {
       char G4_LDS* xb = smem + C::kLdsX;
-      xchg_write(xb, wave * C::kXPer, lane, sacc);
-      if constexpr (DK) xchg_write(xb, wave * C::kXPer + 1, lane, pacc);
+#pragma unroll
+      for (int kp = 0; kp < KPW; ++kp) {
+        xchg_write(xb, (wave * KPW + kp) * C::kXPer, lane, sacc[kp]);
+        if constexpr (DK) xchg_write(xb, (wave * KPW + kp) * C::kXPer + 1, lane, pacc[kp]);
+      }
       barrier_lds();
-      // Single dO buffer: every wave's dP reads are retired; refill it now.
-      if constexpr (!C::kDoDouble)
-        if (it + 1 < nsteps) issue_do(it + 1, 0);
-      xchg_add(xb, (wave ^ 1) * C::kXPer, lane, dh, sacc);
-      if constexpr (DK) xchg_add(xb, (wave ^ 1) * C::kXPer + 1, lane, dh, pacc);
+      // Single-buffered tiles: every wave's reads of them are retired.
+      if (it + 1 < nsteps) {
+        if constexpr (!C::kQDouble) issue_q(it + 1, 0);
+        if constexpr (!C::kDoDouble) issue_do(it + 1, 0);
+      }
+#pragma unroll
+      for (int kp = 0; kp < KPW; ++kp) {
+        xchg_add(xb, ((wave ^ 1) * KPW + kp) * C::kXPer, lane, dh, sacc[kp]);
+        if constexpr (DK) xchg_add(xb, ((wave ^ 1) * KPW + kp) * C::kXPer + 1, lane, dh, pacc[kp]);
+      }
     }
 
     // Rows (queries) of the accumulators: 8 (r >> 2) + 4 h32 + (r & 3).
@@ -224,7 +242,7 @@ struct DkdvKernel {
     const bool full = !has_doc && (i0 + C::kBM <= sq.lq) && (j0 + C::kBN <= sq.lk) &&
                       (j0 + C::kBN - 1 <= i0 + off) &&
                       (a->p.window <= 0 || j0 > i0 + C::kBM - 1 + off - a->p.window);
-    bf16x8 pb[2], db[2];
+    bf16x8 pb[KPW][2], db[KPW][2];
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
       const int il0 = 8 * r4 + 4 * h32;
@@ -239,41 +257,46 @@ struct DkdvKernel {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = r4 * 4 + e;
-        float p = fast_exp2(sacc[r] * kLog2e - lse4[e] * kLog2e);
-        if (!full) {
-          const int i = i0 + il0 + e;
-          const int aq = i + off;
-          const bool in_w = a->p.window <= 0 || my_j > aq - a->p.window;
-          const bool causal = my_j <= aq;
-          const bool vis = has_vid & (vq4[e] >= 0) & (vq4[e] == my_vid);
-          const bool doc_ok = !has_doc | (dq4[e] == my_doc);
-          const bool ok = (i < sq.lq) & (my_j < sq.lk) & in_w & (causal | vis) & doc_ok;
-          p = ok ? p : 0.f;
+        const float lse2 = lse4[e] * kLog2e;
+#pragma unroll
+        for (int kp = 0; kp < KPW; ++kp) {
+          float p = fast_exp2(sacc[kp][r] * kLog2e - lse2);
+          if (!full) {
+            const int i = i0 + il0 + e;
+            const int aq = i + off;
+            const int j = my_j[kp];
+            const bool in_w = a->p.window <= 0 || j > aq - a->p.window;
+            const bool causal = j <= aq;
+            const bool vis = has_vid & (vq4[e] >= 0) & (vq4[e] == my_vid[kp]);
+            const bool doc_ok = !has_doc | (dq4[e] == my_doc[kp]);
+            const bool ok = (i < sq.lq) & (j < sq.lk) & in_w & (causal | vis) & doc_ok;
+            p = ok ? p : 0.f;
+          }
+          if constexpr (DV) pb[kp][r >> 3][r & 7] = (__bf16)p;
+          if constexpr (DK) db[kp][r >> 3][r & 7] = (__bf16)(p * (pacc[kp][r] - del4[e]));
         }
-        if constexpr (DV) pb[r >> 3][r & 7] = (__bf16)p;
-        if constexpr (DK) db[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - del4[e]));
       }
     }
 
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (DV) {
-      acc_step<0, 0>(dot, pb[0], dv_acc);
-      acc_step<1, 0>(dot, pb[1], dv_acc);
-      mfma_pipeline_hint<2 * kNB, 6, 2>();
+      acc_step<0, 0>(dot, pb, dv_acc);
+      acc_step<1, 0>(dot, pb, dv_acc);
+      mfma_read_hint<2 * kNB, KPW, 2, 6>();
     }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (DK) {
-      acc_step<0, 0>(qt, db[0], dk_acc);
-      acc_step<1, 0>(qt, db[1], dk_acc);
-      mfma_pipeline_hint<2 * kNB, 6, 2>();
+      acc_step<0, 0>(qt, db, dk_acc);
+      acc_step<1, 0>(qt, db, dk_acc);
+      mfma_read_hint<2 * kNB, KPW, 2, 6>();
     }
     __builtin_amdgcn_sched_barrier(0);
   }
 };
 
-template <int D, int DSPLIT, int NKB, bool META, bool DV, bool DK>
+template <int D, int DSPLIT, int NKB, bool META, bool DV, bool DK, int KPW>
 __global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a) {
-  using K = DkdvKernel<D, DSPLIT, NKB, META, DV, DK>;
+  using K = DkdvKernel<D, DSPLIT, NKB, META, DV, DK, KPW>;
   using C = typename K::C;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   K ker;
@@ -306,8 +329,8 @@ __global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a)
   ker.has_doc = META && p.document_ids != nullptr;
   ker.has_meta = ker.has_vid || ker.has_doc;
   const int j_last = min(ker.j0 + C::kBN, sq.lk) - 1;
-  ker.my_j = ker.j0 + ker.kb * 32 + l32;
-  const int jc = min(ker.my_j, sq.lk - 1);
+#pragma unroll
+  for (int kp = 0; kp < KPW; ++kp) ker.my_j[kp] = ker.j0 + (ker.kb * KPW + kp) * 32 + l32;
 
   // ---- query range of this key tile ---------------------------------------
   int span_min = 0x7fffffff;
@@ -336,25 +359,26 @@ __global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a)
   ker.qcp.init(a.ql.token_stride, ker.wave, ker.lane);
   ker.docp.init(a.dol.token_stride, ker.wave, ker.lane);
 
-  // ---- K / V fragments of this wave's 32 keys (B operands) ---------------
-  {
+  // ---- K / V fragments of this wave's KPW * 32 keys (B operands) ----------
+#pragma unroll
+  for (int kp = 0; kp < KPW; ++kp) {
+    const int jc = min(ker.my_j[kp], sq.lk - 1);
     const __bf16* krow = a.k + tok_off(sq, ker.s, sq.ktok, jc, a.kl) +
                          (int64_t)ker.kvh * a.kl.head_stride + ker.dh * C::kDH + ker.h32 * 8;
     const __bf16* vrow = a.v + tok_off(sq, ker.s, sq.ktok, jc, a.vl) +
                          (int64_t)ker.kvh * a.vl.head_stride + ker.dh * C::kDH + ker.h32 * 8;
 #pragma unroll
     for (int c = 0; c < K::kNC; ++c) {
-      ker.kf[c] = ld_global16(krow + c * 16);
-      if constexpr (DK) ker.vf[c] = ld_global16(vrow + c * 16);
+      ker.kf[kp][c] = ld_global16(krow + c * 16);
+      if constexpr (DK) ker.vf[kp][c] = ld_global16(vrow + c * 16);
     }
-  }
-  ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + jc] : -1;
-  ker.my_doc = ker.has_doc ? p.document_ids[sq.ktok + jc] : 0;
-
+    ker.my_vid[kp] = ker.has_vid ? p.vision_ids[sq.ktok + jc] : -1;
+    ker.my_doc[kp] = ker.has_doc ? p.document_ids[sq.ktok + jc] : 0;
 #pragma unroll
-  for (int b = 0; b < K::kNB; ++b) {
-    if constexpr (DK) ker.dk_acc[b] = f32x16{};
-    if constexpr (DV) ker.dv_acc[b] = f32x16{};
+    for (int b = 0; b < K::kNB; ++b) {
+      if constexpr (DK) ker.dk_acc[kp][b] = f32x16{};
+      if constexpr (DV) ker.dv_acc[kp][b] = f32x16{};
+    }
   }
 
   if (nsteps > 0) {
@@ -367,10 +391,13 @@ __global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a)
   }
 
   // ---- write dK, dV (bf16), 4 consecutive head-dim elements per store --------
-  if (ker.my_j < sq.lk) {
-    __bf16* dkrow = a.dk + tok_off(sq, ker.s, sq.ktok, ker.my_j, a.dkl) +
+#pragma unroll
+  for (int kp = 0; kp < KPW; ++kp) {
+    const int j = ker.my_j[kp];
+    if (j >= sq.lk) continue;
+    __bf16* dkrow = a.dk + tok_off(sq, ker.s, sq.ktok, j, a.dkl) +
                     (int64_t)ker.kvh * a.dkl.head_stride;
-    __bf16* dvrow = a.dv + tok_off(sq, ker.s, sq.ktok, ker.my_j, a.dvl) +
+    __bf16* dvrow = a.dv + tok_off(sq, ker.s, sq.ktok, j, a.dvl) +
                     (int64_t)ker.kvh * a.dvl.head_stride;
 #pragma unroll
     for (int b = 0; b < K::kNB; ++b)
@@ -378,12 +405,12 @@ __global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a)
       for (int r4 = 0; r4 < 4; ++r4) {
         const int d = ker.dh * C::kDH + b * 32 + 8 * r4 + 4 * ker.h32;
         if constexpr (DK) {
-          const f32x16& x = ker.dk_acc[b];
+          const f32x16& x = ker.dk_acc[kp][b];
           *(bf16x4*)(dkrow + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
                                          (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
         }
         if constexpr (DV) {
-          const f32x16& y = ker.dv_acc[b];
+          const f32x16& y = ker.dv_acc[kp][b];
           *(bf16x4*)(dvrow + d) = bf16x4{(__bf16)y[r4 * 4], (__bf16)y[r4 * 4 + 1],
                                          (__bf16)y[r4 * 4 + 2], (__bf16)y[r4 * 4 + 3]};
         }
@@ -711,12 +738,12 @@ hipError_t set_lds(Kern kern, int bytes, bool& done) {
   return e;
 }
 
-template <int D, int DSPLIT, int NKB, bool DV, bool DK>
+template <int D, int DSPLIT, int NKB, bool DV, bool DK, int KPW>
 hipError_t launch_dkdv_cfg(const BwdParams& a, hipStream_t stream) {
-  using C = DkdvCfg<D, DSPLIT, NKB, DV, DK>;
+  using C = DkdvCfg<D, DSPLIT, NKB, DV, DK, KPW>;
   const bool meta = has_meta(a.p);
-  auto kern = meta ? dkdv_kernel<D, DSPLIT, NKB, true, DV, DK>
-                   : dkdv_kernel<D, DSPLIT, NKB, false, DV, DK>;
+  auto kern = meta ? dkdv_kernel<D, DSPLIT, NKB, true, DV, DK, KPW>
+                   : dkdv_kernel<D, DSPLIT, NKB, false, DV, DK, KPW>;
   static bool done[2] = {false, false};
   hipError_t e = set_lds(kern, C::kLdsBytes, done[meta]);
   if (e != hipSuccess) return e;
@@ -748,12 +775,13 @@ hipError_t launch_dq_cfg(const BwdParams& a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_bwd_dkdv(const BwdParams& a, hipStream_t stream) {
-  if (a.p.head_dim == 256) return launch_dkdv_cfg<256, 1, 4, true, true>(a, stream);
+  if (a.p.head_dim == 256) return launch_dkdv_cfg<256, 1, 4, true, true, 1>(a, stream);
   if (a.p.head_dim == 512) {
-    // d512: dV and dK in two launches (their combined state exceeds 512 VGPRs)
-    hipError_t e = launch_dkdv_cfg<512, 2, 2, true, false>(a, stream);
+    // d512: dV and dK in two launches (their combined state exceeds the
+    // register file).
+    hipError_t e = launch_dkdv_cfg<512, 2, 2, true, false, 1>(a, stream);
     if (e != hipSuccess) return e;
-    return launch_dkdv_cfg<512, 2, 2, false, true>(a, stream);
+    return launch_dkdv_cfg<512, 2, 2, false, true, 1>(a, stream);
   }
   return hipErrorInvalidValue;
 }

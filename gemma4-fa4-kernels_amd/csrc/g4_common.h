@@ -105,37 +105,40 @@ __device__ __forceinline__ void g2l4(const void* gptr, char G4_LDS* lds_wave_bas
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
-// Per-lane LDS offsets for row-wise 16-byte MFMA operand reads of a swizzled
-// tile with CPR chunks per row: lane reads row (row0 + (lane & 31)) and chunk
-// (cbase + 2 c' + (lane >> 5)), c' < 8 * n, row0 and cbase multiples of 16.
-// The XOR of the swizzle only touches the low 4 chunk bits, so the offset
-// splits into one of 8 per-lane registers plus a compile-time immediate.
+// Row-wise 16-byte MFMA operand reads of a swizzled tile with CPR chunks per
+// row: lane reads row (row0 + (lane & 31)) and chunk (cbase + 2 c' + (lane >> 5)),
+// row0 and cbase multiples of 16.  With sw = swz(r), the slot of chunk
+// 2w + h (w < 8) is 2 (w ^ (sw >> 1)) + (h ^ (sw & 1)), so the byte offset is
+// one per-lane base with the constant 32 w XORed into bits 5-7 (which hold
+// sw >> 1): one VGPR and one v_xor per read instead of an offset table.
 template <int CPR>
 struct RowReader {
-  int off[8];
-  // base: byte offset added to every read (e.g. the wave's head-dim slice,
-  // 16 * a multiple of 16 chunks), folded in here so reads are reg + immediate.
-  __device__ __forceinline__ void init(int lane, int base = 0) {
+  int base;
+  // b: byte offset added to every read (e.g. the wave's head-dim slice, a
+  // multiple of 256), folded in here.
+  __device__ __forceinline__ void init(int lane, int b = 0) {
     const int r = lane & 31, h = lane >> 5;
     const int sw = ((r & 3) << 2) | ((r >> 2) & 3);
-#pragma unroll
-    for (int w = 0; w < 8; ++w) off[w] = base + (r * CPR + ((2 * w + h) ^ sw)) * 16;
+    base = b + r * CPR * 16 + 32 * (sw >> 1) + 16 * (h ^ (sw & 1));
   }
   template <int ROW0, int CBASE, int CP>
   __device__ __forceinline__ bf16x8 read(const char G4_LDS* tile) const {
     static_assert(ROW0 % 16 == 0 && CBASE % 16 == 0, "alignment");
-    return *(const bf16x8 G4_LDS*)(tile + off[CP & 7] + (ROW0 * CPR + CBASE + 16 * (CP >> 3)) * 16);
+    const int off = base ^ (32 * (CP & 7));
+    return *(const bf16x8 G4_LDS*)(tile + off + (ROW0 * CPR + CBASE + 16 * (CP >> 3)) * 16);
   }
 };
 
-// Per-lane LDS offsets for the transposing reads that build a 32 x 16 MFMA A
-// operand (rows = 32 columns of the tile starting at chunk cbase + 4 b, k = 16
-// tile rows starting at row0) from a row-major swizzled tile:
-// lane l gets column 16*((l>>4)&1) + (l&15) and rows {4h + e, 8 + 4h + e}.
+// Transposing reads that build a 32 x 16 MFMA A operand (rows = 32 columns of
+// the tile starting at chunk cbase + 4 b, k = 16 tile rows starting at row0)
+// from a row-major swizzled tile: lane l gets column 16*((l>>4)&1) + (l&15)
+// and rows {4h + e, 8 + 4h + e}.  Chunk 4 bq + lb sits in slot
+// 4 (bq ^ (sw >> 2)) + (lb ^ (sw & 3)), so each of the two row groups needs
+// one per-lane base with 64 bq XORed into bits 6-7.
 template <int CPR>
 struct TrReader {
-  int off[2][4];
-  __device__ __forceinline__ void init(int lane, int base = 0) {
+  int base[2];
+  __device__ __forceinline__ void init(int lane, int b = 0) {
     const int g = lane >> 4, sl = lane & 15;
     const int rl = 4 * (g >> 1) + (sl >> 2);
     const int lb = 2 * (g & 1) + ((sl >> 1) & 1);
@@ -144,8 +147,7 @@ struct TrReader {
     for (int e = 0; e < 2; ++e) {
       const int r = rl + 8 * e;
       const int sw = ((r & 3) << 2) | ((r >> 2) & 3);
-#pragma unroll
-      for (int bq = 0; bq < 4; ++bq) off[e][bq] = base + (r * CPR + ((4 * bq + lb) ^ sw)) * 16 + half;
+      base[e] = b + r * CPR * 16 + 64 * (sw >> 2) + 16 * (lb ^ (sw & 3)) + half;
     }
   }
   template <int ROW0, int CBASE, int B>
@@ -153,9 +155,9 @@ struct TrReader {
     static_assert(ROW0 % 16 == 0 && CBASE % 16 == 0, "alignment");
     constexpr int imm = (ROW0 * CPR + CBASE + 16 * (B >> 2)) * 16;
     bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-        (bf16x4 G4_LDS*)(tile + off[0][B & 3] + imm));
+        (bf16x4 G4_LDS*)(tile + (base[0] ^ (64 * (B & 3))) + imm));
     bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-        (bf16x4 G4_LDS*)(tile + off[1][B & 3] + imm));
+        (bf16x4 G4_LDS*)(tile + (base[1] ^ (64 * (B & 3))) + imm));
     return cat4(lo, hi);
   }
 };
@@ -258,6 +260,19 @@ __device__ __forceinline__ void mfma_pipeline_hint() {
   for (int i = 0; i < N; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);
+  }
+}
+
+// Scheduling hint for NR operand reads of DPR DS instructions each, every
+// read feeding MPR MFMAs: PRE DS instructions first, then (MPR MFMAs, DPR DS
+// instructions) repeated.  Region delimited by sched_barrier(0).
+template <int NR, int MPR, int DPR, int PRE>
+__device__ __forceinline__ void mfma_read_hint() {
+  __builtin_amdgcn_sched_group_barrier(0x100, PRE, 0);
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, MPR, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, DPR, 0);
   }
 }
 
