@@ -63,6 +63,9 @@ int check_operand(const void* ptr, const g4_layout& l, const char* name) {
       l.batch_stride < 0 || l.batch_stride % 8)
     return fail(G4_ERR_INVALID, "operand %s strides must be positive multiples of 8 elements",
                 name);
+  // Tile copies form the in-tile part of their addresses as 32-bit offsets.
+  if (l.token_stride >= (int64_t(1) << 24))
+    return fail(G4_ERR_INVALID, "operand %s token stride must be below 2^24 elements", name);
   return G4_OK;
 }
 

@@ -19,8 +19,6 @@
 //
 // With DSPLIT = 2 (head dim 512) the two waves of a pair own the two halves of
 // the head dimension and exchange their partial S / dP through LDS.
-#include <type_traits>
-
 #include "g4_kernels.h"
 
 namespace g4 {
@@ -108,10 +106,7 @@ struct DkdvKernel {
   int64_t tq;
   RowReader<C::kCPR> rrd;
   TrReader<C::kCPR> trd;
-  // 64-chunk rows (head dim 512): the copy row is wave-uniform, so no
-  // per-lane offset tables are needed.
-  using Copier = std::conditional_t<C::kCPR == 64, RowTileCopier<32, C::kNW>,
-                                    TileCopier<C::kCPR, 32, C::kNW>>;
+  using Copier = TileCopier<C::kCPR, 32, C::kNW>;
   Copier qcp, docp;
   bf16x8 kf[KPW][kNC];
   bf16x8 vf[KPW][DK ? kNC : 1];
@@ -154,16 +149,23 @@ struct DkdvKernel {
   __device__ __forceinline__ void issue_rows(int it, int buf) {
     int qh, i0;
     coords(it, qh, i0);
+    // Each half-wave copies from one array (uniform base pointer, exec-masked
+    // issue); lane l lands in LDS slot l either way.
     const int i = min(i0 + (lane & 31), sq.lq - 1);
     if (wave == 0) {
-      const float* src = lane < 32 ? a->lse + lse_off(a->p, sq, s, qh, i)
-                                   : a->delta + (int64_t)qh * tq + sq.qtok + i;
-      g2l4(src, smem + C::kLdsLd + buf * 256);
+      char G4_LDS* dst = smem + C::kLdsLd + buf * 256;
+      if (lane < 32)
+        g2l4(a->lse + lse_off(a->p, sq, s, qh, i), dst);
+      else
+        g2l4(a->delta + (int64_t)qh * tq + sq.qtok + i, dst);
     } else if (wave == 1 && has_meta) {
+      char G4_LDS* dst = smem + C::kLdsMeta + buf * 256;
       const int64_t kidx = sq.ktok + i + off;
-      const int* src = lane < 32 ? (has_vid ? a->p.vision_ids + kidx : a->p.document_ids + kidx)
-                                 : (has_doc ? a->p.document_ids + kidx : a->p.vision_ids + kidx);
-      g2l4(src, smem + C::kLdsMeta + buf * 256);
+      if (lane < 32) {
+        if (has_vid) g2l4(a->p.vision_ids + kidx, dst);
+      } else {
+        if (has_doc) g2l4(a->p.document_ids + kidx, dst);
+      }
     }
   }
 

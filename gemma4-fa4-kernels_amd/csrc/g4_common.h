@@ -97,6 +97,15 @@ __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Async 16-byte buffer -> LDS copy from a wave-uniform base with a 32-bit
+// per-lane byte offset (raw buffer, no stride, 2 GiB range): lane l writes LDS
+// bytes [lds_wave_base + 16 l, +16).  The offset stays a single 32-bit VGPR.
+__device__ __forceinline__ void b2l16(const void* base, uint32_t voff, char G4_LDS* lds_wave_base) {
+  __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (void G4_LDS*)lds_wave_base, 16, voff, 0, 0, 0);
+}
+
 // Async 4-byte global -> LDS copy: lane l writes LDS bytes [base + 4 l, +4).
 __device__ __forceinline__ void g2l4(const void* gptr, char G4_LDS* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(gptr, (void G4_LDS*)lds_wave_base, 4, 0, 0);
@@ -162,88 +171,59 @@ struct TrReader {
   }
 };
 
-// Async copy of a BN-row tile of a row-major operand (rows of CPR 16-byte
-// chunks) into a swizzled LDS tile by NW waves.  Per-lane byte offsets of the
-// chunks relative to the tile's first row are precomputed; the tile base is a
-// wave-uniform pointer.
+// Async copy of a BN-row tile of a row-major operand (rows of CPR = 32 or 64
+// 16-byte chunks) into a swizzled LDS tile by NW waves.  Copy instruction i
+// of a wave fills LDS bytes [1 KB * u, +1 KB) with u = i * NW + wave: rows
+// u * (64 / CPR) + lane / CPR, chunk slot lane % CPR.  The row is wave-uniform
+// up to lane / CPR, so addresses are formed at issue time (scalar row math plus
+// a couple of VALU ops) instead of from per-lane offset tables, which keeps
+// copies from pinning VGPRs that would otherwise spill.
 template <int CPR, int BN, int NW>
 struct TileCopier {
+  static_assert(CPR == 32 || CPR == 64, "rows of 32 or 64 chunks");
+  static constexpr int kRows = 64 / CPR;  // rows per copy instruction
   static constexpr int kPer = BN * CPR / (64 * NW);
   static_assert(kPer * 64 * NW == BN * CPR, "tile must split evenly over the waves");
-  uint32_t goff[kPer];  // byte offset of this lane's chunk i relative to the tile's first row
   int wave, lane;
   int64_t stride_bytes;
-  __device__ __forceinline__ void chunk(int i, int& r, int& c) const {
-    const int p = (i * NW + wave) * 64 + lane;
-    r = p / CPR;
-    c = (p % CPR) ^ (((r & 3) << 2) | ((r >> 2) & 3));
-  }
   __device__ __forceinline__ void init(int64_t row_stride_elems, int wave_, int lane_) {
     wave = wave_;
     lane = lane_;
     stride_bytes = row_stride_elems * 2;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      int r, c;
-      chunk(i, r, c);
-      goff[i] = (uint32_t)(r * stride_bytes + c * 16);
-    }
   }
-  // rows row0 .. row0 + BN - 1 must all exist.
+  // rows row0 .. row0 + BN - 1 must all exist.  The scalar base carries the
+  // instruction's first row; the per-lane offset (row within the instruction,
+  // chunk column) is a 32-bit buffer offset for 32-chunk rows, where a 64-bit
+  // per-lane address would be hoisted out of loops and spilled (the C ABI
+  // bounds token strides below 2^24 elements, so offsets stay below 2^31).
   __device__ __forceinline__ void issue(const __bf16* tile_row0, char G4_LDS* tile) const {
     const char* g = (const char*)tile_row0;
+    const int lr = lane / CPR, lc = lane % CPR;
+    const uint32_t lane_row = (uint32_t)lr * (uint32_t)stride_bytes;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) g2l16(g + goff[i], tile + (i * NW + wave) * 64 * 16);
+    for (int i = 0; i < kPer; ++i) {
+      const int u = i * NW + wave;
+      const int r = u * kRows + lr;
+      const uint32_t c = lc ^ (((r & 3) << 2) | ((r >> 2) & 3));
+      const char* row = g + (int64_t)(u * kRows) * stride_bytes;
+      if constexpr (CPR == 64)
+        g2l16(row + c * 16u, tile + u * 1024);  // lane_row == 0: offset is lane ^ const
+      else
+        b2l16(row, lane_row + c * 16u, tile + u * 1024);
+    }
   }
   // Tail tile: rows >= nrows are replaced by row nrows - 1 (their scores are
   // masked, so they only need to be finite data).
   __device__ __forceinline__ void issue_clamped(const __bf16* tile_row0, int64_t, int nrows,
-                                                char G4_LDS* tile, int, int) const {
-    const char* g = (const char*)tile_row0;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      int r, c;
-      chunk(i, r, c);
-      g2l16(g + (int64_t)min(r, nrows - 1) * stride_bytes + c * 16,
-            tile + (i * NW + wave) * 64 * 16);
-    }
-  }
-};
-
-// Async copy of a BN-row tile whose rows are exactly 64 16-byte chunks (head
-// dim 512) by NW waves, without per-lane offset tables: chunk i of a lane
-// belongs to the wave-uniform row i * NW + wave, so only the swizzled column
-// (lane ^ swz(row)) is per-lane and is formed at issue time.
-template <int BN, int NW>
-struct RowTileCopier {
-  static constexpr int kPer = BN / NW;
-  static_assert(kPer * NW == BN, "tile must split evenly over the waves");
-  int wave, lane;
-  int64_t stride_bytes;
-  __device__ __forceinline__ void init(int64_t row_stride_elems, int wave_, int lane_) {
-    wave = wave_;
-    lane = lane_;
-    stride_bytes = row_stride_elems * 2;
-  }
-  __device__ __forceinline__ void issue(const __bf16* tile_row0, char G4_LDS* tile) const {
-    const char* g = (const char*)tile_row0;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int r = i * NW + wave;
-      const int c = lane ^ (((r & 3) << 2) | ((r >> 2) & 3));
-      g2l16(g + r * stride_bytes + c * 16, tile + r * 64 * 16);
-    }
-  }
-  // Tail tile: rows >= nrows are replaced by row nrows - 1.  (The trailing
-  // arguments match TileCopier::issue_clamped.)
-  __device__ __forceinline__ void issue_clamped(const __bf16* tile_row0, int64_t, int nrows,
                                                 char G4_LDS* tile, int = 0, int = 0) const {
     const char* g = (const char*)tile_row0;
+    const int lr = lane / CPR, lc = lane % CPR;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int r = i * NW + wave;
-      const int c = lane ^ (((r & 3) << 2) | ((r >> 2) & 3));
-      g2l16(g + (int64_t)min(r, nrows - 1) * stride_bytes + c * 16, tile + r * 64 * 16);
+      const int u = i * NW + wave;
+      const int r = u * kRows + lr;
+      const uint32_t c = lc ^ (((r & 3) << 2) | ((r >> 2) & 3));
+      b2l16(g, (uint32_t)min(r, nrows - 1) * (uint32_t)stride_bytes + c * 16u, tile + u * 1024);
     }
   }
 };

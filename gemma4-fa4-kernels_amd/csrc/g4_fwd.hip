@@ -462,7 +462,7 @@ struct FwdWide {
   int64_t kstride, vstride;
   RowReader<C::kCPR> krd;
   TrReader<C::kCPR> vrd;
-  RowTileCopier<BN, C::kNW> kcp, vcp;
+  TileCopier<C::kCPR, BN, C::kNW> kcp, vcp;
   bf16x8 qf[kNC];
   f32x16 o_acc[kNB];
   float m_run, l_run;
