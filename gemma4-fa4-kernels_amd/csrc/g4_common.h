@@ -178,7 +178,9 @@ struct TrReader {
 // up to lane / CPR, so addresses are formed at issue time (scalar row math plus
 // a couple of VALU ops) instead of from per-lane offset tables, which keeps
 // copies from pinning VGPRs that would otherwise spill.
-template <int CPR, int BN, int NW>
+// FRESH: re-form the per-lane offsets at every issue (see fresh_lane), for
+// kernels whose register budget cannot hold them across a loop.
+template <int CPR, int BN, int NW, bool FRESH = false>
 struct TileCopier {
   static_assert(CPR == 32 || CPR == 64, "rows of 32 or 64 chunks");
   static constexpr int kRows = 64 / CPR;  // rows per copy instruction
@@ -196,9 +198,18 @@ struct TileCopier {
   // chunk column) is a 32-bit buffer offset for 32-chunk rows, where a 64-bit
   // per-lane address would be hoisted out of loops and spilled (the C ABI
   // bounds token strides below 2^24 elements, so offsets stay below 2^31).
+  // With FRESH the lane id is passed through an empty asm so the per-lane
+  // offsets are formed at each issue (a few VALU ops) rather than hoisted out
+  // of the caller's loop into registers that would then be spilled.
+  __device__ __forceinline__ int fresh_lane() const {
+    int l = lane;
+    if constexpr (FRESH) asm volatile("" : "+v"(l));
+    return l;
+  }
   __device__ __forceinline__ void issue(const __bf16* tile_row0, char G4_LDS* tile) const {
     const char* g = (const char*)tile_row0;
-    const int lr = lane / CPR, lc = lane % CPR;
+    const int ln = fresh_lane();
+    const int lr = ln / CPR, lc = ln % CPR;
     const uint32_t lane_row = (uint32_t)lr * (uint32_t)stride_bytes;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
@@ -217,7 +228,8 @@ struct TileCopier {
   __device__ __forceinline__ void issue_clamped(const __bf16* tile_row0, int64_t, int nrows,
                                                 char G4_LDS* tile, int = 0, int = 0) const {
     const char* g = (const char*)tile_row0;
-    const int lr = lane / CPR, lc = lane % CPR;
+    const int ln = fresh_lane();
+    const int lr = ln / CPR, lc = ln % CPR;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int u = i * NW + wave;

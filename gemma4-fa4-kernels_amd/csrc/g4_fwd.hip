@@ -47,7 +47,7 @@ __device__ __forceinline__ void issue_meta(const g4_problem& p, const Seq& sq, i
   if (p.document_ids != nullptr) g2l4(p.document_ids + idx, dst + 256);
 }
 
-template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META>
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META, int OCC = 1>
 struct FwdKernel {
   using C = FwdCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
   static constexpr int kNB = C::kDH / 32;  // 32-wide head-dim blocks per wave
@@ -65,7 +65,7 @@ struct FwdKernel {
   int64_t kstride, vstride;
   RowReader<C::kCPR> krd;
   TrReader<C::kCPR> vrd;
-  TileCopier<C::kCPR, BN, C::kNW> kcp, vcp;
+  TileCopier<C::kCPR, BN, C::kNW, (OCC > 1)> kcp, vcp;
   bf16x8 qf[kNC];
   f32x16 o_acc[kNB];
   float m_run, l_run;
@@ -255,9 +255,11 @@ struct FwdKernel {
 };
 
 // FIXUP: rerun only the 32-query groups the wide kernel flagged in raise_flags.
-template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META, bool FIXUP = false>
-__global__ void __launch_bounds__(NQG * DSPLIT * 64, 1) fwd_kernel(FwdParams a) {
-  using K = FwdKernel<D, BN, DSPLIT, NQG, VDOUBLE, META>;
+// OCC: workgroups per CU the register budget is sized for.
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META, bool FIXUP = false,
+          int OCC = 1>
+__global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a) {
+  using K = FwdKernel<D, BN, DSPLIT, NQG, VDOUBLE, META, OCC>;
   using C = typename K::C;
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   K ker;
@@ -698,14 +700,14 @@ static hipError_t launch_fwd_wide(const FwdParams& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE>
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, int OCC = 1>
 static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fixup = false) {
   using C = FwdCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
   const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
                     a.p.document_ids != nullptr;
-  auto kern = meta    ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, true>
-              : fixup ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false, true>
-                      : fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false>;
+  auto kern = meta    ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, true, false, OCC>
+              : fixup ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false, true, OCC>
+                      : fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false, false, OCC>;
   const int variant = meta ? 1 : fixup ? 2 : 0;
   static bool attr_set[3] = {false, false, false};
   if (!attr_set[variant]) {
@@ -723,7 +725,15 @@ static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fi
 }
 
 hipError_t launch_fwd(const FwdParams& a, hipStream_t stream) {
-  if (a.p.head_dim == 256) return launch_fwd_cfg<256, 64, 1, 4, true>(a, stream);
+  if (a.p.head_dim == 256) {
+    // Without key metadata two workgroups of 32-key tiles share a CU (the
+    // register file holds two waves per SIMD); the vision / document mask
+    // needs more registers and runs one workgroup of 64-key tiles per CU.
+    const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
+                      a.p.document_ids != nullptr;
+    if (!meta) return launch_fwd_cfg<256, 32, 1, 4, true, 2>(a, stream);
+    return launch_fwd_cfg<256, 64, 1, 4, true, 1>(a, stream);
+  }
   if (a.p.head_dim == 512) {
     const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
                       a.p.document_ids != nullptr;
