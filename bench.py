@@ -9,14 +9,18 @@ path the reference benchmark uses for this shape (bench_attention.py:80-133,
 350-359): fa4_global_varlen_forward with cu_seqlens = [0, S], then
 torch.autograd.backward(out, dO).  Throughput is mask-aware TFLOP/s from the
 reference FLOP model (reference.py:331-356): fwd 2*Hq*P*(Dqk+Dv),
-bwd 2*Hq*P*(3*Dqk+2*Dv), P = S(S+1)/2 allowed pairs per head.
+bwd 2*Hq*P*(3*Dqk+2*Dv), P = allowed pairs per head (S(S+1)/2 here).
 
-Also reported (not `value`): forward-only and backward-only times, the local
-d256 sliding-window configurations, per-kernel times measured with HIP events
-on the launch stream (the roofline of the dominant kernel), and the fp32 CPU
-oracle timed on a bounded sample of the same workload on this host.
+Also reported (not `value`): forward-only and backward-only times with
+quartiles, the same call with cold caches, the other four configurations
+(gemma4_fa4_amd.workloads: local S=2048 forward, local multimodal S=8192,
+packed global T=32768 backward, packed local T=131072 with vision blocks and
+documents; P counted exactly per row), per-kernel times measured with HIP
+events on the launch stream (the roofline of the dominant kernel), and the
+fp32 CPU oracle timed on a bounded sample of configuration 2 on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       [--no-extra]
 """
 
 from __future__ import annotations
@@ -80,53 +84,77 @@ def event_times(torch, fn, reps: int, warm: int):
     return out
 
 
-def run_case(torch, g, *, kind: str, s: int, steps: int, warmup: int, seed: int, dev):
-    """Time fwd, bwd and fwd+bwd of one configuration through the drop-in adapters."""
-    hq, hkv, d = (32, 16, 256) if kind == "local" else (32, 4, 512)
-    q, k, v, do = make_inputs(torch, seed, s, hq, hkv, d, dev)
-    cu = torch.tensor([0, s], dtype=torch.int32, device=dev)
-    fn_name = "fa4_local_varlen_forward" if kind == "local" else "fa4_global_varlen_forward"
-    attn = getattr(g, fn_name)
+def _stats(samples):
+    q = statistics.quantiles(samples, n=4) if len(samples) > 1 else [samples[0]] * 3
+    return {"median": statistics.median(samples), "p25": q[0], "p75": q[2]}
 
-    def fwd():
-        with torch.no_grad():
-            attn(q, k, v, cu, cu, max_seqlen_q=s, max_seqlen_k=s)
 
-    def fwd_bwd():
-        qi, ki, vi = (t.detach().requires_grad_(True) for t in (q, k, v))
-        out, _lse = attn(qi, ki, vi, cu, cu, max_seqlen_q=s, max_seqlen_k=s)
-        torch.autograd.backward(out, do)
+def run_workload(torch, g, w, *, steps: int, warmup: int, dev, flush=None):
+    """Time the timed modes of one workload through the drop-in packed adapters.
+
+    fwd: forward with autograd off; bwd: torch.autograd.backward of a forward
+    recorded just before (forward excluded); fwd_bwd: both.  Medians with the
+    quartiles; with `flush`, every timed call is preceded by a write of a
+    buffer larger than the L2 and Infinity Cache (cold caches).
+    """
+    from gemma4_fa4_amd import workloads as wl
+
+    q, k, v, do, cu, vis, docs = wl.tensors(w, dev)
+    mq = max(w.seg_lengths)
+    if w.kind == "local":
+        def attn(qi, ki, vi):
+            return g.fa4_local_varlen_forward(qi, ki, vi, cu, cu, max_seqlen_q=mq,
+                                              max_seqlen_k=mq, vision_block_ids=vis,
+                                              document_ids=docs)
+    else:
+        def attn(qi, ki, vi):
+            return g.fa4_global_varlen_forward(qi, ki, vi, cu, cu, max_seqlen_q=mq,
+                                               max_seqlen_k=mq)
+
+    def fresh():
+        return [t.detach().requires_grad_(True) for t in (q, k, v)]
 
     state = {}
 
-    def prep_bwd():
-        qi, ki, vi = (t.detach().requires_grad_(True) for t in (q, k, v))
-        out, _lse = attn(qi, ki, vi, cu, cu, max_seqlen_q=s, max_seqlen_k=s)
-        state["out"] = out
+    def fwd():
+        with torch.no_grad():
+            attn(q, k, v)
+
+    def prep():
+        state["out"], _ = attn(*fresh())
 
     def bwd():
         torch.autograd.backward(state["out"], do)
 
-    pairs = pairs_window(s, 1024) if kind == "local" else pairs_causal(s)
-    res = {"kind": kind, "seqlen": s, "pairs_per_head": pairs}
-    t_fwd = event_times(torch, fwd, steps, warmup)
-    bwd_samples = []
-    for i in range(warmup + steps):
-        prep_bwd()
-        torch.cuda.synchronize()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        bwd()
-        b.record()
-        b.synchronize()
-        if i >= warmup:
-            bwd_samples.append(a.elapsed_time(b))
-    t_fb = event_times(torch, fwd_bwd, steps, warmup)
-    for mode, samples in (("fwd", t_fwd), ("bwd", bwd_samples), ("fwd_bwd", t_fb)):
-        ms = statistics.median(samples)
-        tf = flops(pairs, hq, d, mode) / (ms * 1e-3) / 1e12
-        res[f"{mode}_ms"] = round(ms, 4)
+    def fwd_bwd():
+        out, _ = attn(*fresh())
+        torch.autograd.backward(out, do)
+
+    pairs = wl.allowed_pairs(w)
+    res = {"kind": w.kind, "tokens": w.tokens, "segments": len(w.seg_lengths),
+           "pairs_per_head": pairs, "text_pairs_per_head": wl.text_pairs(w),
+           "vision_tokens": 0 if w.vision is None else int((w.vision >= 0).sum()),
+           "seed": w.seed}
+    for mode in w.modes:
+        samples = []
+        for i in range(warmup + steps):
+            if mode == "bwd":
+                prep()
+            if flush is not None:
+                flush()
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            {"fwd": fwd, "bwd": bwd, "fwd_bwd": fwd_bwd}[mode]()
+            b.record()
+            b.synchronize()
+            if i >= warmup:
+                samples.append(a.elapsed_time(b))
+        st = _stats(samples)
+        tf = flops(pairs, w.hq, w.d, mode) / (st["median"] * 1e-3) / 1e12
+        res[f"{mode}_ms"] = round(st["median"], 4)
+        res[f"{mode}_ms_p25_p75"] = [round(st["p25"], 4), round(st["p75"], 4)]
         res[f"{mode}_tflops"] = round(tf, 2)
         res[f"{mode}_pct_peak"] = round(100.0 * tf / PEAK_BF16_TFLOPS, 2)
     return res, (q, k, v, do, cu)
@@ -256,11 +284,12 @@ def cpu_baseline(budget_s: float):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--no-extra", action="store_true", help="skip the local d256 configurations")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="only configuration 2 (skip configurations 1, 3, 4, 5 and the cold-cache run)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): this build "
@@ -271,20 +300,29 @@ def main() -> int:
     import torch
     import gemma4_fa4_amd as g
 
+    from gemma4_fa4_amd import workloads as wl
+
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     s = 8192
-    head, tensors = run_case(torch, g, kind="global", s=s, steps=args.steps,
-                             warmup=args.warmup, seed=0, dev=dev)
+    head, tensors = run_workload(torch, g, wl.config2(), steps=args.steps, warmup=args.warmup,
+                                 dev=dev)
     roofline, per_kernel, delta_gbs, copy_gbs = kernel_roofline(torch, g, tensors, s=s,
                                                                 reps=max(3, args.steps))
     extra = {}
     if not args.no_extra:
-        c1, _ = run_case(torch, g, kind="local", s=2048, steps=args.steps, warmup=args.warmup,
-                         seed=1, dev=dev)
-        l8, _ = run_case(torch, g, kind="local", s=8192, steps=args.steps, warmup=args.warmup,
-                         seed=2, dev=dev)
-        extra = {"local_d256_S2048": c1, "local_d256_S8192": l8}
+        # Cold caches: a 1 GiB write (4x the 256 MB Infinity Cache) before each call.
+        junk = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        cold, _ = run_workload(torch, g, wl.config2(), steps=max(3, args.steps // 2),
+                               warmup=1, dev=dev, flush=lambda: junk.fill_(1))
+        head["fwd_bwd_cold_ms"] = cold["fwd_bwd_ms"]
+        head["fwd_bwd_cold_tflops"] = cold["fwd_bwd_tflops"]
+        del junk
+        for cfg in (wl.config1, wl.config3, wl.config4, wl.config5):
+            w = cfg()
+            extra[w.name], _ = run_workload(torch, g, w, steps=args.steps,
+                                            warmup=args.warmup, dev=dev)
+            torch.cuda.empty_cache()
     value = head["fwd_bwd_tflops"]
     line = {
         "metric": "mask-aware TFLOP/s fwd/bwd (d256 sliding, d512 global, S=8192) + % bf16 MFMA peak",
@@ -307,7 +345,7 @@ def main() -> int:
             "seq_len": s,
             "pct_bf16_peak": head["fwd_bwd_pct_peak"],
         },
-        "global_d512_S8192": head,
+        "config2_global_d512_S8192_fwd_bwd": head,
         "per_kernel_ms": per_kernel,
         "bwd_delta_gbs": delta_gbs,
         "calibration_copy_gbs": copy_gbs,
