@@ -47,7 +47,8 @@ __device__ __forceinline__ void issue_meta(const g4_problem& p, const Seq& sq, i
   if (p.document_ids != nullptr) g2l4(p.document_ids + idx, dst + 256);
 }
 
-template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META, int OCC = 1>
+// META: key metadata kinds compiled in (bit 0 vision IDs, bit 1 document IDs).
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, int META, int OCC = 1>
 struct FwdKernel {
   using C = FwdCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
   static constexpr int kNB = C::kDH / 32;  // 32-wide head-dim blocks per wave
@@ -205,7 +206,11 @@ struct FwdKernel {
     for (int kb = 0; kb < C::kKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[kb][r] *= kLog2e;
-    if (!full) apply_mask(cur, sacc, kb0);
+    if (!full) {
+      __builtin_amdgcn_sched_barrier(0);
+      apply_mask(cur, sacc, kb0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     float mx = kNegInf;
 #pragma unroll
     for (int kb = 0; kb < C::kKB; ++kb)
@@ -256,7 +261,7 @@ struct FwdKernel {
 
 // FIXUP: rerun only the 32-query groups the wide kernel flagged in raise_flags.
 // OCC: workgroups per CU the register budget is sized for.
-template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META, bool FIXUP = false,
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, int META, bool FIXUP = false,
           int OCC = 1>
 __global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a) {
   using K = FwdKernel<D, BN, DSPLIT, NQG, VDOUBLE, META, OCC>;
@@ -303,8 +308,8 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a
   const int off = sq.lk - sq.lq;  // query i sits at key position i + off
   ker.a0 = i0 + off;
   const int a_last_valid = min(i0 + C::kBM, sq.lq) - 1 + off;
-  ker.has_vid = META && p.vision_ids != nullptr && p.bidirectional_vision;
-  ker.has_doc = META && p.document_ids != nullptr;
+  ker.has_vid = (META & 1) && p.vision_ids != nullptr && p.bidirectional_vision;
+  ker.has_doc = (META & 2) && p.document_ids != nullptr;
   ker.has_meta = ker.has_vid || ker.has_doc;
 
   // ---- key range (mask-aware tile scheduler) -------------------------------
@@ -700,16 +705,24 @@ static hipError_t launch_fwd_wide(const FwdParams& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Key metadata kinds a problem carries (bit 0 vision IDs, bit 1 document IDs).
+static int meta_kind(const g4_problem& p) {
+  return ((p.vision_ids != nullptr && p.bidirectional_vision) ? 1 : 0) |
+         (p.document_ids != nullptr ? 2 : 0);
+}
+
 template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, int OCC = 1>
 static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fixup = false) {
   using C = FwdCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
-  const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
-                    a.p.document_ids != nullptr;
-  auto kern = meta    ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, true, false, OCC>
-              : fixup ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false, true, OCC>
-                      : fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, false, false, OCC>;
-  const int variant = meta ? 1 : fixup ? 2 : 0;
-  static bool attr_set[3] = {false, false, false};
+  const int meta = meta_kind(a.p);
+  void (*kern)(FwdParams) =
+      meta == 1   ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, 1, false, OCC>
+      : meta == 2 ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, 2, false, OCC>
+      : meta == 3 ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, 3, false, OCC>
+      : fixup     ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, 0, true, OCC>
+                  : fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, 0, false, OCC>;
+  const int variant = fixup ? 4 : meta;
+  static bool attr_set[5] = {false, false, false, false, false};
   if (!attr_set[variant]) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
@@ -726,18 +739,15 @@ static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fi
 
 hipError_t launch_fwd(const FwdParams& a, hipStream_t stream) {
   if (a.p.head_dim == 256) {
-    // Without key metadata two workgroups of 32-key tiles share a CU (the
-    // register file holds two waves per SIMD); the vision / document mask
-    // needs more registers and runs one workgroup of 64-key tiles per CU.
-    const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
-                      a.p.document_ids != nullptr;
-    if (!meta) return launch_fwd_cfg<256, 32, 1, 4, true, 2>(a, stream);
+    // Two workgroups of 32-key tiles share a CU (the register file holds two
+    // waves per SIMD), except with both vision and document IDs, whose mask
+    // state needs one workgroup of 64-key tiles per CU.
+    if (meta_kind(a.p) != 3) return launch_fwd_cfg<256, 32, 1, 4, true, 2>(a, stream);
     return launch_fwd_cfg<256, 64, 1, 4, true, 1>(a, stream);
   }
   if (a.p.head_dim == 512) {
-    const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
-                      a.p.document_ids != nullptr;
-    if (meta || a.raise_flags == nullptr) return launch_fwd_cfg<512, 32, 2, 2, true>(a, stream);
+    if (meta_kind(a.p) != 0 || a.raise_flags == nullptr)
+      return launch_fwd_cfg<512, 32, 2, 2, true>(a, stream);
     // Fast pass, then the rescaling kernel on the 32-query groups it flagged.
     hipError_t e = launch_fwd_wide<512>(a, stream);
     if (e != hipSuccess) return e;
