@@ -354,6 +354,14 @@ __global__ void __launch_bounds__(NKB * DSPLIT * 64, 1) dkdv_kernel(BwdParams a)
   key_tile_query_range(ker.j0, j_last, sq.lq, ker.off, p.window, span_min, ilo, ihi);
   ker.qt_lo = ilo / C::kBM;
   ker.nqt = ihi > ilo ? (ihi + C::kBM - 1) / C::kBM - ker.qt_lo : 0;
+  if (ker.has_doc && ker.nqt > 0 &&
+      doc_uniform<C::kNW>(p.document_ids, sq.ktok, sq.lk,
+                          min(ker.j0, ker.qt_lo * C::kBM + ker.off),
+                          max(j_last + 1, (ker.qt_lo + ker.nqt) * C::kBM + ker.off), tid,
+                          ker.lane, ker.wave, (int*)(smem_raw + C::kLdsRed))) {
+    ker.has_doc = false;
+    ker.has_meta = ker.has_vid;
+  }
   const int nsteps = ker.nqt * ker.grp;
 
   ker.rrd.init(ker.lane, ker.dh * C::kDH * 2);
@@ -444,10 +452,10 @@ struct DqCfg {
 };
 
 __device__ __forceinline__ void issue_key_meta(const g4_problem& p, const Seq& sq, int j0,
-                                               char G4_LDS* dst, int lane) {
+                                               char G4_LDS* dst, int lane, bool vid, bool doc) {
   const int64_t idx = sq.ktok + min(j0 + lane, sq.lk - 1);
-  if (p.vision_ids != nullptr && p.bidirectional_vision) g2l4(p.vision_ids + idx, dst);
-  if (p.document_ids != nullptr) g2l4(p.document_ids + idx, dst + 256);
+  if (vid) g2l4(p.vision_ids + idx, dst);
+  if (doc) g2l4(p.document_ids + idx, dst + 256);
 }
 
 template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META>
@@ -519,7 +527,8 @@ struct DqKernel {
     if (it + 1 < ntiles) {
       issue_k(kb0 + BN, cur ^ 1);
       if (has_meta && wave == 0)
-        issue_key_meta(a->p, sq, kb0 + BN, smem + C::kLdsMeta + (cur ^ 1) * 512, lane);
+        issue_key_meta(a->p, sq, kb0 + BN, smem + C::kLdsMeta + (cur ^ 1) * 512, lane,
+                       has_vid, has_doc);
       if constexpr (VDOUBLE) issue_v(kb0 + BN, cur ^ 1);
     }
     const char G4_LDS* kt = smem + C::kLdsK + cur * C::kTile;
@@ -664,6 +673,13 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, 1) dq_kernel(BwdParams a) {
   query_tile_key_range(ker.a0, a_last_valid, sq.lk, p.window, span_max, klo, khi);
   const int t_first = klo / BN;
   const int ntiles = (khi + BN - 1) / BN - t_first;
+  if (ker.has_doc &&
+      doc_uniform<C::kNW>(p.document_ids, sq.ktok, sq.lk, min(t_first * BN, ker.a0),
+                          max((t_first + ntiles) * BN, a_last_valid + 1), tid, ker.lane,
+                          ker.wave, (int*)(smem_raw + C::kLdsRed))) {
+    ker.has_doc = false;
+    ker.has_meta = ker.has_vid;
+  }
 
   ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
   ker.vbase = a.v + tok_off(sq, s, sq.ktok, 0, a.vl) + (int64_t)kvh * a.vl.head_stride;
@@ -700,7 +716,8 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, 1) dq_kernel(BwdParams a) {
   if (ntiles > 0) {
     ker.issue_k(t_first * BN, 0);
     if (ker.has_meta && ker.wave == 0)
-      issue_key_meta(p, sq, t_first * BN, ker.smem + C::kLdsMeta, ker.lane);
+      issue_key_meta(p, sq, t_first * BN, ker.smem + C::kLdsMeta, ker.lane, ker.has_vid,
+                     ker.has_doc);
     ker.issue_v(t_first * BN, 0);
   }
   for (int it = 0; it < ntiles; ++it) {

@@ -302,6 +302,33 @@ __device__ __forceinline__ int64_t tok_off(const Seq& sq, int s, int64_t seq_tok
                    : (int64_t)s * L.batch_stride + (int64_t)t * L.token_stride;
 }
 
+// True when every K-stream position [lo, hi) of a sequence (clamped to its
+// lk keys) carries one document ID.  A workgroup whose queries and visited
+// key tiles all lie in such a range sees the document predicate admit every
+// pair it visits, so it drops the predicate (and its per-tile ID copies)
+// exactly.  The range must span whole visited tiles, not only the scheduled
+// key range: vision spans are per (document, vision ID), so a tile's tail
+// past the range can hold keys of the same vision block in another document.  Every thread of the workgroup calls
+// this; `red` is one int per wave of LDS, free on entry.
+template <int NW>
+__device__ __forceinline__ bool doc_uniform(const int* doc, int64_t ktok, int lk, int lo, int hi,
+                                            int tid, int lane, int wave, int* red) {
+  lo = max(lo, 0);
+  hi = min(hi, lk);
+  if (lo >= hi) return true;
+  const int ref = doc[ktok + lo];
+  bool diff = false;
+  for (int t = lo + tid; t < hi; t += NW * 64) diff |= doc[ktok + t] != ref;
+  const bool wave_diff = __ballot(diff) != 0;  // every lane votes (outside the lane-0 branch)
+  barrier_lds();  // earlier readers of red are done
+  if (lane == 0) red[wave] = wave_diff;
+  barrier_lds();
+  int any = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) any |= red[w];
+  return any == 0;
+}
+
 // Tokens in the Q stream (packed total, or num_seqs * seqlen_q).
 __device__ __forceinline__ int64_t q_stream_tokens_dev(const g4_problem& p) {
   return p.cu_seqlens_q ? p.total_q : (int64_t)p.num_seqs * p.seqlen_q;

@@ -41,10 +41,10 @@ struct FwdCfg {
 // Async copy of the vision / document IDs of keys [j0, j0 + 64) of a sequence
 // (clamped to its last key; keys past the end are masked by index).
 __device__ __forceinline__ void issue_meta(const g4_problem& p, const Seq& sq, int j0,
-                                           char G4_LDS* dst, int lane) {
+                                           char G4_LDS* dst, int lane, bool vid, bool doc) {
   const int64_t idx = sq.ktok + min(j0 + lane, sq.lk - 1);
-  if (p.vision_ids != nullptr && p.bidirectional_vision) g2l4(p.vision_ids + idx, dst);
-  if (p.document_ids != nullptr) g2l4(p.document_ids + idx, dst + 256);
+  if (vid) g2l4(p.vision_ids + idx, dst);
+  if (doc) g2l4(p.document_ids + idx, dst + 256);
 }
 
 // META: key metadata kinds compiled in (bit 0 vision IDs, bit 1 document IDs).
@@ -147,7 +147,7 @@ struct FwdKernel {
     barrier_lds();
     if (it + 1 < ntiles) {
       issue_k(kb0 + BN, cur ^ 1);
-      if (has_meta && wave == 0) issue_meta(*p, sq, kb0 + BN, smem + C::kLdsMeta + (cur ^ 1) * 512, lane);
+      if (has_meta && wave == 0) issue_meta(*p, sq, kb0 + BN, smem + C::kLdsMeta + (cur ^ 1) * 512, lane, has_vid, has_doc);
       if constexpr (VDOUBLE) issue_v(kb0 + BN, cur ^ 1);
     }
 
@@ -332,6 +332,20 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a
   query_tile_key_range(ker.a0, a_last_valid, sq.lk, p.window, span_max, klo, khi);
   const int t_first = klo / BN;
   const int ntiles = (khi + BN - 1) / BN - t_first;
+  // ---- document uniformity -------------------------------------------------
+  // The range spans whole 64-key tiles (a superset of the visited tiles for
+  // BN <= 64), so both launches of a split problem evaluate it identically.
+  if (p.document_ids != nullptr && (ker.has_doc || a.doc_pass == 1)) {
+    const bool uni = doc_uniform<C::kNW>(
+        p.document_ids, sq.ktok, sq.lk, min(klo / 64 * 64, ker.a0),
+        max((khi + 63) / 64 * 64, a_last_valid + 1), ker.tid, ker.lane, ker.wave,
+        (int*)(smem_raw + C::kLdsRed));
+    if ((a.doc_pass == 1 && !uni) || (a.doc_pass == 2 && uni)) return;
+    if (uni) {
+      ker.has_doc = false;
+      ker.has_meta = ker.has_vid;
+    }
+  }
 
   // ---- operand bases, address tables ---------------------------------------
   ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
@@ -364,7 +378,7 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a
   // ---- prologue: tile 0 (issue order K, key metadata, V) -----------------
   if (ntiles > 0) {
     ker.issue_k(t_first * BN, 0);
-    if (ker.has_meta && ker.wave == 0) issue_meta(p, sq, t_first * BN, ker.smem + C::kLdsMeta, ker.lane);
+    if (ker.has_meta && ker.wave == 0) issue_meta(p, sq, t_first * BN, ker.smem + C::kLdsMeta, ker.lane, ker.has_vid, ker.has_doc);
     ker.issue_v(t_first * BN, 0);
   }
 
@@ -711,10 +725,12 @@ static int meta_kind(const g4_problem& p) {
          (p.document_ids != nullptr ? 2 : 0);
 }
 
+// meta < 0: the problem's own metadata kinds; doc_pass: see FwdParams.
 template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, int OCC = 1>
-static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fixup = false) {
+static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fixup = false,
+                                 int meta_override = -1, int doc_pass = 0) {
   using C = FwdCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
-  const int meta = meta_kind(a.p);
+  const int meta = meta_override >= 0 ? meta_override : meta_kind(a.p);
   void (*kern)(FwdParams) =
       meta == 1   ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, 1, false, OCC>
       : meta == 2 ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, 2, false, OCC>
@@ -731,6 +747,7 @@ static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fi
   }
   FwdParams b = a;
   b.ntq = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
+  b.doc_pass = doc_pass;
   const int64_t nblocks = (int64_t)b.num_seqs * b.ntq * a.p.num_q_heads;
   if (nblocks <= 0) return hipSuccess;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
@@ -740,10 +757,18 @@ static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fi
 hipError_t launch_fwd(const FwdParams& a, hipStream_t stream) {
   if (a.p.head_dim == 256) {
     // Two workgroups of 32-key tiles share a CU (the register file holds two
-    // waves per SIMD), except with both vision and document IDs, whose mask
-    // state needs one workgroup of 64-key tiles per CU.
+    // waves per SIMD).  With both vision and document IDs the mask state needs
+    // one workgroup of 64-key tiles per CU, so such a problem is split: the
+    // query tiles that see a single document run in the vision-only kernel,
+    // the rest in the full-mask one.
     if (meta_kind(a.p) != 3) return launch_fwd_cfg<256, 32, 1, 4, true, 2>(a, stream);
-    return launch_fwd_cfg<256, 64, 1, 4, true, 1>(a, stream);
+    static_assert(FwdCfg<256, 32, 1, 4, true>::kBM == FwdCfg<256, 64, 1, 4, true>::kBM,
+                  "both passes must tile queries alike");
+    hipError_t e = launch_fwd_cfg<256, 32, 1, 4, true, 2>(a, stream, false, /*meta=*/1,
+                                                          /*doc_pass=*/1);
+    if (e != hipSuccess) return e;
+    return launch_fwd_cfg<256, 64, 1, 4, true, 1>(a, stream, false, /*meta=*/3,
+                                                  /*doc_pass=*/2);
   }
   if (a.p.head_dim == 512) {
     if (meta_kind(a.p) != 0 || a.raise_flags == nullptr)

@@ -18,6 +18,10 @@ struct FwdParams {
   int num_seqs;
   int ntq;             // query tiles per sequence (set by the launcher)
   int* raise_flags;    // per (seq, 32-query group, head): rows the fast pass cannot finish
+  // Split of a problem with document IDs over two launches (set by the
+  // launcher): 0 every workgroup; 1 only workgroups whose queries and visited
+  // keys share one document (their document test is dropped); 2 the others.
+  int doc_pass;
 };
 
 struct BwdParams {

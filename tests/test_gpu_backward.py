@@ -179,3 +179,33 @@ def test_structured_ownership_of_local_gradients():
         assert torch.count_nonzero(other) == 0
         assert torch.count_nonzero(grad[64, kvh]) > 0
         assert torch.count_nonzero(grad[65, kvh]) == 0
+
+
+@pytest.mark.parametrize("lq,lk,cuts", [
+    ([2600], [2600], [900, 1700]),
+    ([1500, 1800], [1900, 1800], [1210, 2600, 3300]),
+])
+def test_local_documents_with_vision_blocks_across_boundaries(lq, lk, cuts):
+    """Long runs of one document (where a workgroup drops the document test)
+    next to vision blocks that straddle document boundaries: a vision block
+    cut by a boundary is two spans, and the tile tails past a span must still
+    see the document test."""
+    g = _g()
+    q, k, v, do, dlse = qkv(7000 + sum(lq), sum(lq), sum(lk), 32, 16, 256)
+    t = sum(lk)
+    docs = torch.zeros(t, dtype=torch.int32)
+    for n, c in enumerate(cuts):
+        docs[c:] = n + 1
+    vis = torch.full((t,), -1, dtype=torch.int32)
+    for b, c in enumerate(cuts):
+        vis[c - 70 - 13 * b: c + 45 + 7 * b] = b  # straddles the boundary at c
+    cq, ck = cu(lq), cu(lk)
+    qd, kd, vd = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
+    o, lse = g.fa4_local_varlen_forward(
+        qd, kd, vd, cq.to(DEV), ck.to(DEV), max_seqlen_q=max(lq), max_seqlen_k=max(lk),
+        vision_block_ids=vis.to(DEV), document_ids=docs.to(DEV))
+    ((o.float() * do.to(DEV).float()).sum() + (lse * dlse.to(DEV)).sum()).backward()
+    (o_ref, l_ref, *refs), bf = _oracle(q, k, v, cq, ck, do, dlse, window=1024, vision=vis,
+                                        docs=docs)
+    check_forward(o.detach(), lse.detach(), o_ref, l_ref, local=True, label=f"docs {cuts}")
+    check_gradients([qd.grad, kd.grad, vd.grad], refs, bf, label=f"docs {cuts}")
