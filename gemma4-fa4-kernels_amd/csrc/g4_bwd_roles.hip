@@ -1,0 +1,415 @@
+// dK / dV for head dim 512 on gfx950 with role-specialised waves.
+//
+// A workgroup owns 64 keys (two blocks of 32) of one KV head and runs eight
+// waves, two per SIMD.  Four P waves (one per key block and head-dim half)
+// form S = Q K^T, P = exp(S - LSE) and accumulate dV^T += dO^T P; four dS
+// waves form dP = dO V^T, dS = P (dP - delta) and accumulate dK^T += Q^T dS.
+// Each wave holds one 32-key x 256 fp32 accumulator and one fragment set (K or
+// V) in registers, so the two roles together keep the state one wave of head
+// dim 512 cannot; S and dP are formed once per step and the Q / dO tiles are
+// copied once for both outputs.  On each SIMD a P wave and a dS wave share the
+// matrix core, so one's VALU and LDS work overlaps the other's MFMAs.
+//
+// A step is 32 query rows of one query head (steps walk the query tiles from
+// the last one down, the GQA group's heads innermost) with three workgroup
+// barriers:
+//   B1  the step's Q, dO, LSE / delta (and metadata) copies have landed in
+//       every wave; the next step's copies go out into the other buffers.
+//       P waves: partial S over their head-dim half, then write the eight rows
+//       per lane the partner finishes.  dS waves: partial dP, write all 16.
+//   B2  P waves: add the partner's partial to their eight rows, form P (masked)
+//       and publish it in fp32 over the partial they just read.  dS waves: add
+//       the partner's dP partial.
+//   B3  P waves: dV MFMAs with both halves of P in bf16.  dS waves: dS from the
+//       fp32 P, dK MFMAs.
+// P in fp32 and the fixed-order dP sum keep the numerics of a single-wave
+// formulation: dS = bf16(P (dP - delta)), dV from bf16(P).  No atomics; every
+// output element is written by one wave.
+#include "g4_kernels.h"
+
+namespace g4 {
+
+namespace {
+
+struct RolesCfg {
+  static constexpr int D = 512;
+  static constexpr int kNW = 8;
+  static constexpr int kNT = kNW * 64;
+  static constexpr int kBN = 64;   // keys per workgroup
+  static constexpr int kBM = 32;   // queries per step
+  static constexpr int kDH = 256;  // head-dim half per wave
+  static constexpr int kCPR = D / 8;
+  static constexpr int kNC = kDH / 16;  // 16-deep MFMA steps over a half
+  static constexpr int kNB = kDH / 32;  // 32-wide accumulator blocks over a half
+  static constexpr int kTile = kBM * D * 2;  // Q or dO tile bytes
+  static constexpr int kLdsQ = 0;                      // [2 buf] Q tiles
+  static constexpr int kLdsDo = kLdsQ + 2 * kTile;     // [2 buf] dO tiles
+  // P-wave exchange: [slot = 2 kb + dh][2][64 lanes][4 f32]: the partner's
+  // partial S for the slot owner's rows, then the owner's P for those rows.
+  static constexpr int kLdsXs = kLdsDo + 2 * kTile;
+  // dS-wave exchange: [slot][4][64 lanes][4 f32] partial dP.
+  static constexpr int kLdsXp = kLdsXs + 4 * 2 * 1024;
+  static constexpr int kLdsLd = kLdsXp + 4 * 4 * 1024;  // [buf][lse x 32 | delta x 32] fp32
+  static constexpr int kLdsMeta = kLdsLd + 2 * 256;     // [buf][vid x 32 | doc x 32] int32
+  static constexpr int kLdsRed = kLdsMeta + 2 * 256;
+  static constexpr int kLdsBytes = kLdsRed + 64;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+};
+
+template <bool META>
+struct RolesKernel {
+  using C = RolesCfg;
+  char G4_LDS* smem;
+  const BwdParams* a;
+  Seq sq;
+  int s, lane, wave, dh, h32, kb, slot;
+  int off, j0, my_j;
+  bool has_vid, has_doc, has_meta;
+  int my_vid, my_doc;
+  int grp, kvh, qt_lo, nqt;
+  int64_t tq;
+  RowReader<C::kCPR> rrd;
+  TrReader<C::kCPR> trd;
+  TileCopier<C::kCPR, C::kBM, C::kNW> qcp, docp;
+  bf16x8 frag[C::kNC];   // K (P waves) or V (dS waves), B operands
+  f32x16 acc[C::kNB];    // dV^T (P waves) or dK^T (dS waves)
+
+  __device__ __forceinline__ void coords(int it, int& qh, int& i0) const {
+    const int sh = __builtin_ctz(grp);  // grp is 1, 2, 4 or 8
+    qh = kvh * grp + (it & (grp - 1));
+    i0 = (qt_lo + nqt - 1 - (it >> sh)) * C::kBM;
+  }
+
+  __device__ __forceinline__ void issue(int it, int buf) {
+    int qh, i0;
+    coords(it, qh, i0);
+    const __bf16* qb = a->q + tok_off(sq, s, sq.qtok, i0, a->ql) + (int64_t)qh * a->ql.head_stride;
+    const __bf16* db =
+        a->dout + tok_off(sq, s, sq.qtok, i0, a->dol) + (int64_t)qh * a->dol.head_stride;
+    char G4_LDS* qd = smem + C::kLdsQ + buf * C::kTile;
+    char G4_LDS* dd = smem + C::kLdsDo + buf * C::kTile;
+    if (i0 + C::kBM <= sq.lq) {
+      qcp.issue(qb, qd);
+      docp.issue(db, dd);
+    } else {
+      qcp.issue_clamped(qb, a->ql.token_stride, sq.lq - i0, qd);
+      docp.issue_clamped(db, a->dol.token_stride, sq.lq - i0, dd);
+    }
+    // LSE (lanes 0-31) and delta (lanes 32-63) of the 32 rows; with metadata
+    // the vision / document IDs of the rows' K positions.
+    const int i = min(i0 + (lane & 31), sq.lq - 1);
+    if (wave == 0) {
+      char G4_LDS* dst = smem + C::kLdsLd + buf * 256;
+      if (lane < 32)
+        g2l4(a->lse + lse_off(a->p, sq, s, qh, i), dst);
+      else
+        g2l4(a->delta + (int64_t)qh * tq + sq.qtok + i, dst);
+    } else if (wave == 1 && has_meta) {
+      char G4_LDS* dst = smem + C::kLdsMeta + buf * 256;
+      const int64_t kidx = sq.ktok + i + off;
+      if (lane < 32) {
+        if (has_vid) g2l4(a->p.vision_ids + kidx, dst);
+      } else {
+        if (has_doc) g2l4(a->p.document_ids + kidx, dst);
+      }
+    }
+  }
+
+  // acc^T[32 d x 32 keys] += (tile^T half dh)[32 d x 32 rows] . b[32 rows x 32 keys]
+  template <int M, int B>
+  __device__ __forceinline__ void acc_step(const char G4_LDS* t, const bf16x8 (&b)[2]) {
+    if constexpr (B < C::kNB) {
+      bf16x8 x = trd.template read<16 * M, 0, B>(t);
+      acc[B] = mfma32(x, b[M], acc[B]);
+      acc_step<M, B + 1>(t, b);
+    }
+  }
+  // part[32 rows x 32 keys] = tile rows (head-dim half dh) . frag
+  template <int CP>
+  __device__ __forceinline__ void row_step(const char G4_LDS* t, f32x16& part) const {
+    if constexpr (CP < C::kNC) {
+      bf16x8 x = rrd.template read<0, 0, CP>(t);
+      part = mfma32(x, frag[CP], part);
+      row_step<CP + 1>(t, part);
+    }
+  }
+
+  // Rows of the accumulators: value r of a lane is query row 8 (r >> 2) +
+  // 4 h32 + (r & 3); P waves finish rows r in [8 dh, 8 dh + 8).
+  __device__ __forceinline__ char G4_LDS* xs(int sl, int q4) const {
+    return smem + C::kLdsXs + ((sl * 2 + q4) * 64 + lane) * 16;
+  }
+
+  __device__ __forceinline__ void step_p(int cur, int it, int nsteps) {
+    int qh, i0;
+    coords(it, qh, i0);
+    vm_wait<0>();
+    barrier_lds();  // B1
+    if (it + 1 < nsteps) issue(it + 1, cur ^ 1);
+    const char G4_LDS* qt = smem + C::kLdsQ + cur * C::kTile;
+    const char G4_LDS* dot = smem + C::kLdsDo + cur * C::kTile;
+
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 sp = f32x16{};
+    row_step<0>(qt, sp);
+    mfma_read_hint<C::kNC, 1, 1, 3>();
+    __builtin_amdgcn_sched_barrier(0);
+    // the partner's rows of this partial
+    const int po = 8 * (dh ^ 1);
+#pragma unroll
+    for (int q4 = 0; q4 < 2; ++q4)
+      *(f32x4 G4_LDS*)xs(slot ^ 1, q4) =
+          f32x4{sp[po + 4 * q4], sp[po + 4 * q4 + 1], sp[po + 4 * q4 + 2], sp[po + 4 * q4 + 3]};
+    barrier_lds();  // B2
+
+    const float* ld = (const float*)(smem + C::kLdsLd + cur * 256);
+    const bool full = !has_doc && (i0 + C::kBM <= sq.lq) && (j0 + C::kBN <= sq.lk) &&
+                      (j0 + C::kBN - 1 <= i0 + off) &&
+                      (a->p.window <= 0 || j0 > i0 + C::kBM - 1 + off - a->p.window);
+    const int mo = 8 * dh;
+#pragma unroll
+    for (int q4 = 0; q4 < 2; ++q4) {
+      const f32x4 theirs = *(const f32x4 G4_LDS*)xs(slot, q4);
+      const int r4 = 2 * dh + q4;
+      const int il0 = 8 * r4 + 4 * h32;
+      const f32x4 lse4 = *(const f32x4*)(ld + il0);
+      i32x4 vq4 = {-1, -1, -1, -1}, dq4 = {0, 0, 0, 0};
+      if (has_meta && !full) {
+        const int* mt = (const int*)(smem + C::kLdsMeta + cur * 256);
+        vq4 = *(const i32x4*)(mt + il0);
+        dq4 = *(const i32x4*)(mt + 32 + il0);
+      }
+      f32x4 pv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float sv = sp[mo + 4 * q4 + e] + theirs[e];
+        float p = fast_exp2(sv * kLog2e - lse4[e] * kLog2e);
+        if (!full) {
+          const int i = i0 + il0 + e;
+          const int aq = i + off;
+          const bool in_w = a->p.window <= 0 || my_j > aq - a->p.window;
+          const bool causal = my_j <= aq;
+          const bool vis = has_vid & (vq4[e] >= 0) & (vq4[e] == my_vid);
+          const bool doc_ok = !has_doc | (dq4[e] == my_doc);
+          const bool ok = (i < sq.lq) & (my_j < sq.lk) & in_w & (causal | vis) & doc_ok;
+          p = ok ? p : 0.f;
+        }
+        pv[e] = p;
+      }
+      // Same address as `theirs` (read first in this wave's LDS order).
+      *(f32x4 G4_LDS*)xs(slot, q4) = pv;
+    }
+    barrier_lds();  // B3
+
+    bf16x8 pb[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int q4 = 0; q4 < 2; ++q4) {
+        const f32x4 v = *(const f32x4 G4_LDS*)xs((slot & ~1) | m, q4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pb[m][4 * q4 + e] = (__bf16)v[e];
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    acc_step<0, 0>(dot, pb);
+    acc_step<1, 0>(dot, pb);
+    mfma_read_hint<2 * C::kNB, 1, 2, 6>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  __device__ __forceinline__ void step_ds(int cur, int it, int nsteps) {
+    vm_wait<0>();
+    barrier_lds();  // B1
+    if (it + 1 < nsteps) issue(it + 1, cur ^ 1);
+    const char G4_LDS* qt = smem + C::kLdsQ + cur * C::kTile;
+    const char G4_LDS* dot = smem + C::kLdsDo + cur * C::kTile;
+    char G4_LDS* xp = smem + C::kLdsXp;
+
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 dp = f32x16{};
+    row_step<0>(dot, dp);
+    mfma_read_hint<C::kNC, 1, 1, 3>();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+      *(f32x4 G4_LDS*)(xp + ((slot * 4 + q4) * 64 + lane) * 16) =
+          f32x4{dp[4 * q4], dp[4 * q4 + 1], dp[4 * q4 + 2], dp[4 * q4 + 3]};
+    barrier_lds();  // B2
+
+    // dP = (slice 0 partial) + (slice 1 partial) in both waves of the pair.
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const f32x4 w = *(const f32x4 G4_LDS*)(xp + (((slot ^ 1) * 4 + q4) * 64 + lane) * 16);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float mine = dp[4 * q4 + e];
+        dp[4 * q4 + e] = dh == 0 ? mine + w[e] : w[e] + mine;
+      }
+    }
+    barrier_lds();  // B3
+
+    const float* ld = (const float*)(smem + C::kLdsLd + cur * 256);
+    bf16x8 db[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int q4 = 0; q4 < 2; ++q4) {
+        const f32x4 pv = *(const f32x4 G4_LDS*)xs((slot & ~1) | m, q4);
+        const f32x4 del4 = *(const f32x4*)(ld + 32 + 8 * (2 * m + q4) + 4 * h32);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 8 * m + 4 * q4 + e;
+          db[m][4 * q4 + e] = (__bf16)(pv[e] * (dp[r] - del4[e]));
+        }
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    acc_step<0, 0>(qt, db);
+    acc_step<1, 0>(qt, db);
+    mfma_read_hint<2 * C::kNB, 1, 2, 6>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Load this wave's K or V fragments, run the steps, store dV or dK (bf16).
+  template <bool PWAVE>
+  __device__ __forceinline__ void run(int nsteps) {
+    const int jc = min(my_j, sq.lk - 1);
+    const __bf16* src = PWAVE ? a->k + tok_off(sq, s, sq.ktok, jc, a->kl) +
+                                    (int64_t)kvh * a->kl.head_stride
+                              : a->v + tok_off(sq, s, sq.ktok, jc, a->vl) +
+                                    (int64_t)kvh * a->vl.head_stride;
+    src += dh * C::kDH + h32 * 8;
+#pragma unroll
+    for (int c = 0; c < C::kNC; ++c) frag[c] = ld_global16(src + c * 16);
+#pragma unroll
+    for (int b = 0; b < C::kNB; ++b) acc[b] = f32x16{};
+
+    for (int it = 0; it < nsteps; ++it) {
+      if constexpr (PWAVE)
+        step_p(it & 1, it, nsteps);
+      else
+        step_ds(it & 1, it, nsteps);
+    }
+
+    if (my_j >= sq.lk) return;
+    __bf16* dst = PWAVE ? a->dv + tok_off(sq, s, sq.ktok, my_j, a->dvl) +
+                              (int64_t)kvh * a->dvl.head_stride
+                        : a->dk + tok_off(sq, s, sq.ktok, my_j, a->dkl) +
+                              (int64_t)kvh * a->dkl.head_stride;
+#pragma unroll
+    for (int b = 0; b < C::kNB; ++b)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = dh * C::kDH + b * 32 + 8 * r4 + 4 * h32;
+        const f32x16& x = acc[b];
+        *(bf16x4*)(dst + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
+                                     (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
+      }
+  }
+};
+
+template <bool META>
+__global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams a) {
+  using K = RolesKernel<META>;
+  using C = RolesCfg;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  K ker;
+  ker.smem = (char G4_LDS*)smem_raw;
+  ker.a = &a;
+  const g4_problem& p = a.p;
+  const int tid = threadIdx.x;
+  ker.lane = tid & 63;
+  ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool pwave = ker.wave < 4;
+  ker.slot = ker.wave & 3;  // 2 kb + dh
+  ker.kb = ker.slot >> 1;
+  ker.dh = ker.slot & 1;
+  ker.h32 = ker.lane >> 5;
+
+  // ---- work item: (sequence, key tile, KV head) ------------------------------
+  ker.grp = p.num_q_heads / p.num_kv_heads;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_kvh = a.num_seqs * a.ntiles;
+  ker.kvh = L / per_kvh;
+  const int rank = L % per_kvh;
+  ker.s = rank / a.ntiles;
+  const int kt = zigzag(rank % a.ntiles, a.ntiles);
+  ker.sq = resolve_seq(p, ker.s);
+  const Seq& sq = ker.sq;
+  ker.j0 = kt * C::kBN;
+  if (ker.j0 >= sq.lk) return;
+  ker.off = sq.lk - sq.lq;
+  ker.tq = q_stream_tokens_dev(p);
+  ker.has_vid = META && p.vision_ids != nullptr && p.bidirectional_vision;
+  ker.has_doc = META && p.document_ids != nullptr;
+  ker.has_meta = ker.has_vid || ker.has_doc;
+  const int j_last = min(ker.j0 + C::kBN, sq.lk) - 1;
+  ker.my_j = ker.j0 + ker.kb * 32 + (ker.lane & 31);
+
+  // ---- query range of this key tile ---------------------------------------
+  int span_min = 0x7fffffff;
+  if (ker.has_vid) {
+    int* red = (int*)(smem_raw + C::kLdsRed);
+    int v = 0x7fffffff;
+    for (int t = tid; t < C::kBN; t += C::kNT) {
+      int j = ker.j0 + t;
+      if (j < sq.lk) v = min(v, a.span_lo[sq.ktok + j]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+    if (ker.lane == 0) red[ker.wave] = v;
+    barrier_lds();
+#pragma unroll
+    for (int w = 0; w < C::kNW; ++w) span_min = min(span_min, red[w]);
+  }
+  int ilo, ihi;
+  key_tile_query_range(ker.j0, j_last, sq.lq, ker.off, p.window, span_min, ilo, ihi);
+  ker.qt_lo = ilo / C::kBM;
+  ker.nqt = ihi > ilo ? (ihi + C::kBM - 1) / C::kBM - ker.qt_lo : 0;
+  if (ker.has_doc && ker.nqt > 0 &&
+      doc_uniform<C::kNW>(p.document_ids, sq.ktok, sq.lk,
+                          min(ker.j0, ker.qt_lo * C::kBM + ker.off),
+                          max(j_last + 1, (ker.qt_lo + ker.nqt) * C::kBM + ker.off), tid,
+                          ker.lane, ker.wave, (int*)(smem_raw + C::kLdsRed))) {
+    ker.has_doc = false;
+    ker.has_meta = ker.has_vid;
+  }
+  const int nsteps = ker.nqt * ker.grp;
+  const int jc = min(ker.my_j, sq.lk - 1);
+  ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + jc] : -1;
+  ker.my_doc = ker.has_doc ? p.document_ids[sq.ktok + jc] : 0;
+
+  ker.rrd.init(ker.lane, ker.dh * C::kDH * 2);
+  ker.trd.init(ker.lane, ker.dh * C::kDH * 2);
+  ker.qcp.init(a.ql.token_stride, ker.wave, ker.lane);
+  ker.docp.init(a.dol.token_stride, ker.wave, ker.lane);
+  if (nsteps > 0) ker.issue(0, 0);
+  // Both roles run nsteps steps of three barriers each.
+  if (pwave)
+    ker.template run<true>(nsteps);
+  else
+    ker.template run<false>(nsteps);
+}
+
+}  // namespace
+
+hipError_t launch_dkdv_roles(const BwdParams& a, hipStream_t stream) {
+  using C = RolesCfg;
+  const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
+                    a.p.document_ids != nullptr;
+  auto kern = meta ? dkdv_roles_kernel<true> : dkdv_roles_kernel<false>;
+  static bool done[2] = {false, false};
+  if (!done[meta]) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+    if (e != hipSuccess) return e;
+    done[meta] = true;
+  }
+  BwdParams b = a;
+  b.ntiles = (a.p.seqlen_k + C::kBN - 1) / C::kBN;
+  const int64_t nblocks = (int64_t)b.num_seqs * b.ntiles * a.p.num_kv_heads;
+  if (nblocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
+  return hipGetLastError();
+}
+
+}  // namespace g4

@@ -196,6 +196,58 @@ struct DkdvKernel {
     }
   }
 
+  // P (and dS) of the lane's 16 * KPW scores; rows (queries) of the
+  // accumulators are 8 (r >> 2) + 4 h32 + (r & 3).  MASKED applies the Gemma
+  // predicate (tiles the mask does not fully admit).
+  // Row LSE / delta come from `lse_r` / `del_r` (read ahead) with a head-dim
+  // pair exchange, else straight from the LDS row buffer `ld`.  MODE 0: no
+  // mask; 1: mask; 2: mask unless `full` (one code path, fewer registers).
+  template <int MODE>
+  __device__ __forceinline__ void probs(int cur, int i0, bool full, const float* ld,
+                                        const f32x4 (&lse_r)[4], const f32x4 (&del_r)[4],
+                                        const f32x16 (&sacc)[KPW], const f32x16 (&pacc)[KPW],
+                                        bf16x8 (&pb)[KPW][2], bf16x8 (&db)[KPW][2]) const {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int il0 = 8 * r4 + 4 * h32;
+      f32x4 lse4, del4;
+      if constexpr (DSPLIT > 1) {
+        lse4 = lse_r[r4];
+        del4 = del_r[r4];
+      } else {
+        lse4 = *(const f32x4*)(ld + il0);
+        del4 = *(const f32x4*)(ld + 32 + il0);
+      }
+      i32x4 vq4 = {-1, -1, -1, -1}, dq4 = {0, 0, 0, 0};
+      if (MODE != 0 && has_meta && !(MODE == 2 && full)) {
+        const int* mt = (const int*)(smem + C::kLdsMeta + cur * 256);
+        vq4 = *(const i32x4*)(mt + il0);
+        dq4 = *(const i32x4*)(mt + 32 + il0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = r4 * 4 + e;
+#pragma unroll
+        for (int kp = 0; kp < KPW; ++kp) {
+          float p = fast_exp2(sacc[kp][r] * kLog2e - lse4[e] * kLog2e);
+          if (MODE == 1 || (MODE == 2 && !full)) {
+            const int i = i0 + il0 + e;
+            const int aq = i + off;
+            const int j = my_j[kp];
+            const bool in_w = a->p.window <= 0 || j > aq - a->p.window;
+            const bool causal = j <= aq;
+            const bool vis = has_vid & (vq4[e] >= 0) & (vq4[e] == my_vid[kp]);
+            const bool doc_ok = !has_doc | (dq4[e] == my_doc[kp]);
+            const bool ok = (i < sq.lq) & (j < sq.lk) & in_w & (causal | vis) & doc_ok;
+            p = ok ? p : 0.f;
+          }
+          if constexpr (DV) pb[kp][r >> 3][r & 7] = (__bf16)p;
+          if constexpr (DK) db[kp][r >> 3][r & 7] = (__bf16)(p * (pacc[kp][r] - del4[e]));
+        }
+      }
+    }
+  }
+
   __device__ __forceinline__ void step(int cur, int it, int nsteps) {
     int qh, i0;
     coords(it, qh, i0);
@@ -219,6 +271,10 @@ struct DkdvKernel {
     mfma_read_hint<(DK ? 2 : 1) * kNC, KPW, 1, 3>();
     __builtin_amdgcn_sched_barrier(0);
 
+    // Row LSE (pre-scaled to log2) and delta, read with the partner partials
+    // so one LDS wait covers both.
+    const float* ld = (const float*)(smem + C::kLdsLd + cur * 256);
+    f32x4 lse_r[4], del_r[4];
     if constexpr (DSPLIT > 1) {
       char G4_LDS* xb = smem + C::kLdsX;
 #pragma unroll
@@ -227,6 +283,11 @@ struct DkdvKernel {
         if constexpr (DK) xchg_write(xb, (wave * KPW + kp) * C::kXPer + 1, lane, pacc[kp]);
       }
       barrier_lds();
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        lse_r[r4] = *(const f32x4*)(ld + 8 * r4 + 4 * h32);
+        if constexpr (DK) del_r[r4] = *(const f32x4*)(ld + 32 + 8 * r4 + 4 * h32);
+      }
       // Single-buffered tiles: every wave's reads of them are retired.
       if (it + 1 < nsteps) {
         if constexpr (!C::kQDouble) issue_q(it + 1, 0);
@@ -239,46 +300,16 @@ struct DkdvKernel {
       }
     }
 
-    // Rows (queries) of the accumulators: 8 (r >> 2) + 4 h32 + (r & 3).
-    const float* ld = (const float*)(smem + C::kLdsLd + cur * 256);
     const bool full = !has_doc && (i0 + C::kBM <= sq.lq) && (j0 + C::kBN <= sq.lk) &&
                       (j0 + C::kBN - 1 <= i0 + off) &&
                       (a->p.window <= 0 || j0 > i0 + C::kBM - 1 + off - a->p.window);
     bf16x8 pb[KPW][2], db[KPW][2];
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const int il0 = 8 * r4 + 4 * h32;
-      const f32x4 lse4 = *(const f32x4*)(ld + il0);
-      const f32x4 del4 = *(const f32x4*)(ld + 32 + il0);
-      i32x4 vq4 = {-1, -1, -1, -1}, dq4 = {0, 0, 0, 0};
-      if (has_meta && !full) {
-        const int* mt = (const int*)(smem + C::kLdsMeta + cur * 256);
-        vq4 = *(const i32x4*)(mt + il0);
-        dq4 = *(const i32x4*)(mt + 32 + il0);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = r4 * 4 + e;
-        const float lse2 = lse4[e] * kLog2e;
-#pragma unroll
-        for (int kp = 0; kp < KPW; ++kp) {
-          float p = fast_exp2(sacc[kp][r] * kLog2e - lse2);
-          if (!full) {
-            const int i = i0 + il0 + e;
-            const int aq = i + off;
-            const int j = my_j[kp];
-            const bool in_w = a->p.window <= 0 || j > aq - a->p.window;
-            const bool causal = j <= aq;
-            const bool vis = has_vid & (vq4[e] >= 0) & (vq4[e] == my_vid[kp]);
-            const bool doc_ok = !has_doc | (dq4[e] == my_doc[kp]);
-            const bool ok = (i < sq.lq) & (j < sq.lk) & in_w & (causal | vis) & doc_ok;
-            p = ok ? p : 0.f;
-          }
-          if constexpr (DV) pb[kp][r >> 3][r & 7] = (__bf16)p;
-          if constexpr (DK) db[kp][r >> 3][r & 7] = (__bf16)(p * (pacc[kp][r] - del4[e]));
-        }
-      }
-    }
+    if constexpr (DSPLIT == 1)
+      probs<2>(cur, i0, full, ld, lse_r, del_r, sacc, pacc, pb, db);
+    else if (full)
+      probs<0>(cur, i0, full, ld, lse_r, del_r, sacc, pacc, pb, db);
+    else
+      probs<1>(cur, i0, full, ld, lse_r, del_r, sacc, pacc, pb, db);
 
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (DV) {
@@ -795,13 +826,8 @@ hipError_t launch_dq_cfg(const BwdParams& a, hipStream_t stream) {
 
 hipError_t launch_bwd_dkdv(const BwdParams& a, hipStream_t stream) {
   if (a.p.head_dim == 256) return launch_dkdv_cfg<256, 1, 4, true, true, 1>(a, stream);
-  if (a.p.head_dim == 512) {
-    // d512: dV and dK in two launches (their combined state exceeds the
-    // register file).
-    hipError_t e = launch_dkdv_cfg<512, 2, 2, true, false, 1>(a, stream);
-    if (e != hipSuccess) return e;
-    return launch_dkdv_cfg<512, 2, 2, false, true, 1>(a, stream);
-  }
+  // d512: role-specialised waves (a dV role and a dK role per SIMD).
+  if (a.p.head_dim == 512) return launch_dkdv_roles(a, stream);
   return hipErrorInvalidValue;
 }
 
