@@ -86,15 +86,11 @@ struct RolesKernel {
     const __bf16* qb = a->q + tok_off(sq, s, sq.qtok, i0, a->ql) + (int64_t)qh * a->ql.head_stride;
     const __bf16* db =
         a->dout + tok_off(sq, s, sq.qtok, i0, a->dol) + (int64_t)qh * a->dol.head_stride;
-    char G4_LDS* qd = smem + C::kLdsQ + buf * C::kTile;
-    char G4_LDS* dd = smem + C::kLdsDo + buf * C::kTile;
-    if (i0 + C::kBM <= sq.lq) {
-      qcp.issue(qb, qd);
-      docp.issue(db, dd);
-    } else {
-      qcp.issue_clamped(qb, a->ql.token_stride, sq.lq - i0, qd);
-      docp.issue_clamped(db, a->dol.token_stride, sq.lq - i0, dd);
-    }
+    // One copy path for full and tail tiles (32-bit buffer offsets, rows
+    // clamped to the sequence): fewer instructions than the full-tile path.
+    const int nr = min(C::kBM, sq.lq - i0);
+    qcp.issue_clamped(qb, a->ql.token_stride, nr, smem + C::kLdsQ + buf * C::kTile);
+    docp.issue_clamped(db, a->dol.token_stride, nr, smem + C::kLdsDo + buf * C::kTile);
     // LSE (lanes 0-31) and delta (lanes 32-63) of the 32 rows; with metadata
     // the vision / document IDs of the rows' K positions.
     const int i = min(i0 + (lane & 31), sq.lq - 1);
@@ -145,12 +141,12 @@ struct RolesKernel {
     coords(it, qh, i0);
     vm_wait<0>();
     barrier_lds();  // B1
-    if (it + 1 < nsteps) issue(it + 1, cur ^ 1);
     const char G4_LDS* qt = smem + C::kLdsQ + cur * C::kTile;
     const char G4_LDS* dot = smem + C::kLdsDo + cur * C::kTile;
 
     __builtin_amdgcn_sched_barrier(0);
     f32x16 sp = f32x16{};
+    if (it + 1 < nsteps) issue(it + 1, cur ^ 1);
     row_step<0>(qt, sp);
     mfma_read_hint<C::kNC, 1, 1, 3>();
     __builtin_amdgcn_sched_barrier(0);
@@ -220,13 +216,13 @@ struct RolesKernel {
   __device__ __forceinline__ void step_ds(int cur, int it, int nsteps) {
     vm_wait<0>();
     barrier_lds();  // B1
-    if (it + 1 < nsteps) issue(it + 1, cur ^ 1);
     const char G4_LDS* qt = smem + C::kLdsQ + cur * C::kTile;
     const char G4_LDS* dot = smem + C::kLdsDo + cur * C::kTile;
     char G4_LDS* xp = smem + C::kLdsXp;
 
     __builtin_amdgcn_sched_barrier(0);
     f32x16 dp = f32x16{};
+    if (it + 1 < nsteps) issue(it + 1, cur ^ 1);
     row_step<0>(dot, dp);
     mfma_read_hint<C::kNC, 1, 1, 3>();
     __builtin_amdgcn_sched_barrier(0);
