@@ -482,13 +482,6 @@ struct DqCfg {
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 };
 
-__device__ __forceinline__ void issue_key_meta(const g4_problem& p, const Seq& sq, int j0,
-                                               char G4_LDS* dst, int lane, bool vid, bool doc) {
-  const int64_t idx = sq.ktok + min(j0 + lane, sq.lk - 1);
-  if (vid) g2l4(p.vision_ids + idx, dst);
-  if (doc) g2l4(p.document_ids + idx, dst + 256);
-}
-
 template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, bool META>
 struct DqKernel {
   using C = DqCfg<D, BN, DSPLIT, NQG, VDOUBLE>;
@@ -833,7 +826,8 @@ hipError_t launch_bwd_dkdv(const BwdParams& a, hipStream_t stream) {
 
 hipError_t launch_bwd_dq(const BwdParams& a, hipStream_t stream) {
   if (a.p.head_dim == 256) return launch_dq_cfg<256, 64, 1, 4, true>(a, stream);
-  if (a.p.head_dim == 512) return launch_dq_cfg<512, 32, 2, 2, false>(a, stream);
+  // d512: role-specialised waves (S waves and dP waves per SIMD).
+  if (a.p.head_dim == 512) return launch_dq_roles(a, stream);
   return hipErrorInvalidValue;
 }
 

@@ -329,6 +329,16 @@ __device__ __forceinline__ bool doc_uniform(const int* doc, int64_t ktok, int lk
   return any == 0;
 }
 
+// Async copy of the vision / document IDs of keys [j0, j0 + 64) of a sequence
+// (clamped to its last key; keys past the end are masked by index) into
+// [vid x 64 | doc x 64] int32 at dst.  One wave issues it.
+__device__ __forceinline__ void issue_key_meta(const g4_problem& p, const Seq& sq, int j0,
+                                               char G4_LDS* dst, int lane, bool vid, bool doc) {
+  const int64_t idx = sq.ktok + min(j0 + lane, sq.lk - 1);
+  if (vid) g2l4(p.vision_ids + idx, dst);
+  if (doc) g2l4(p.document_ids + idx, dst + 256);
+}
+
 // Tokens in the Q stream (packed total, or num_seqs * seqlen_q).
 __device__ __forceinline__ int64_t q_stream_tokens_dev(const g4_problem& p) {
   return p.cu_seqlens_q ? p.total_q : (int64_t)p.num_seqs * p.seqlen_q;
