@@ -14,12 +14,13 @@
 // the last one down, the GQA group's heads innermost) with three workgroup
 // barriers:
 //   B1  the step's Q, dO, LSE / delta (and metadata) copies have landed in
-//       every wave; the next step's copies go out into the other buffers.
-//       P waves: partial S over their head-dim half, then write the eight rows
-//       per lane the partner finishes.  dS waves: partial dP, write all 16.
+//       every wave.  P waves: copy the next Q tile (and row data) into the
+//       other buffer, partial S over their head-dim half, then write the eight
+//       rows per lane the partner finishes.  dS waves: partial dP, write all 16.
 //   B2  P waves: add the partner's partial to their eight rows, form P (masked)
 //       and publish it in fp32 over the partial they just read.  dS waves: add
-//       the partner's dP partial.
+//       the partner's dP partial, then copy the next dO tile (they would
+//       otherwise wait for P here; the copy still lands a phase ahead of B1).
 //   B3  P waves: dV MFMAs with both halves of P in bf16.  dS waves: dS from the
 //       fp32 P, dK MFMAs.
 // P in fp32 and the fixed-order dP sum keep the numerics of a single-wave
@@ -70,7 +71,7 @@ struct RolesKernel {
   int64_t tq;
   RowReader<C::kCPR> rrd;
   TrReader<C::kCPR> trd;
-  TileCopier<C::kCPR, C::kBM, C::kNW> qcp, docp;
+  TileCopier<C::kCPR, C::kBM, 4> qcp, docp;  // Q by the P waves, dO by the dS waves
   bf16x8 frag[C::kNC];   // K (P waves) or V (dS waves), B operands
   f32x16 acc[C::kNB];    // dV^T (P waves) or dK^T (dS waves)
 
@@ -80,19 +81,25 @@ struct RolesKernel {
     i0 = (qt_lo + nqt - 1 - (it >> sh)) * C::kBM;
   }
 
-  __device__ __forceinline__ void issue(int it, int buf) {
+  // One copy path for full and tail tiles (32-bit buffer offsets, rows
+  // clamped to the sequence): fewer instructions than the full-tile path.
+  __device__ __forceinline__ void issue_do(int it, int buf) {
+    int qh, i0;
+    coords(it, qh, i0);
+    const __bf16* db =
+        a->dout + tok_off(sq, s, sq.qtok, i0, a->dol) + (int64_t)qh * a->dol.head_stride;
+    docp.issue_clamped(db, a->dol.token_stride, min(C::kBM, sq.lq - i0),
+                       smem + C::kLdsDo + buf * C::kTile);
+  }
+  // Q tile and, by waves 0 and 1, the row data: LSE (lanes 0-31) and delta
+  // (lanes 32-63) of the 32 rows; with metadata the vision / document IDs of
+  // the rows' K positions.
+  __device__ __forceinline__ void issue_q(int it, int buf) {
     int qh, i0;
     coords(it, qh, i0);
     const __bf16* qb = a->q + tok_off(sq, s, sq.qtok, i0, a->ql) + (int64_t)qh * a->ql.head_stride;
-    const __bf16* db =
-        a->dout + tok_off(sq, s, sq.qtok, i0, a->dol) + (int64_t)qh * a->dol.head_stride;
-    // One copy path for full and tail tiles (32-bit buffer offsets, rows
-    // clamped to the sequence): fewer instructions than the full-tile path.
-    const int nr = min(C::kBM, sq.lq - i0);
-    qcp.issue_clamped(qb, a->ql.token_stride, nr, smem + C::kLdsQ + buf * C::kTile);
-    docp.issue_clamped(db, a->dol.token_stride, nr, smem + C::kLdsDo + buf * C::kTile);
-    // LSE (lanes 0-31) and delta (lanes 32-63) of the 32 rows; with metadata
-    // the vision / document IDs of the rows' K positions.
+    qcp.issue_clamped(qb, a->ql.token_stride, min(C::kBM, sq.lq - i0),
+                      smem + C::kLdsQ + buf * C::kTile);
     const int i = min(i0 + (lane & 31), sq.lq - 1);
     if (wave == 0) {
       char G4_LDS* dst = smem + C::kLdsLd + buf * 256;
@@ -146,7 +153,7 @@ struct RolesKernel {
 
     __builtin_amdgcn_sched_barrier(0);
     f32x16 sp = f32x16{};
-    if (it + 1 < nsteps) issue(it + 1, cur ^ 1);
+    if (it + 1 < nsteps) issue_q(it + 1, cur ^ 1);
     row_step<0>(qt, sp);
     mfma_read_hint<C::kNC, 1, 1, 3>();
     __builtin_amdgcn_sched_barrier(0);
@@ -222,7 +229,6 @@ struct RolesKernel {
 
     __builtin_amdgcn_sched_barrier(0);
     f32x16 dp = f32x16{};
-    if (it + 1 < nsteps) issue(it + 1, cur ^ 1);
     row_step<0>(dot, dp);
     mfma_read_hint<C::kNC, 1, 1, 3>();
     __builtin_amdgcn_sched_barrier(0);
@@ -242,6 +248,7 @@ struct RolesKernel {
         dp[4 * q4 + e] = dh == 0 ? mine + w[e] : w[e] + mine;
       }
     }
+    if (it + 1 < nsteps) issue_do(it + 1, cur ^ 1);
     barrier_lds();  // B3
 
     const float* ld = (const float*)(smem + C::kLdsLd + cur * 256);
@@ -376,9 +383,14 @@ __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams 
 
   ker.rrd.init(ker.lane, ker.dh * C::kDH * 2);
   ker.trd.init(ker.lane, ker.dh * C::kDH * 2);
-  ker.qcp.init(a.ql.token_stride, ker.wave, ker.lane);
-  ker.docp.init(a.dol.token_stride, ker.wave, ker.lane);
-  if (nsteps > 0) ker.issue(0, 0);
+  ker.qcp.init(a.ql.token_stride, ker.wave & 3, ker.lane);
+  ker.docp.init(a.dol.token_stride, ker.wave & 3, ker.lane);
+  if (nsteps > 0) {
+    if (pwave)
+      ker.issue_q(0, 0);
+    else
+      ker.issue_do(0, 0);
+  }
   // Both roles run nsteps steps of three barriers each.
   if (pwave)
     ker.template run<true>(nsteps);
