@@ -26,6 +26,8 @@
 // P in fp32 and the fixed-order dP sum keep the numerics of a single-wave
 // formulation: dS = bf16(P (dP - delta)), dV from bf16(P).  No atomics; every
 // output element is written by one wave.
+#include <type_traits>
+
 #include "g4_kernels.h"
 
 namespace g4 {
@@ -399,6 +401,320 @@ __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams 
 }
 
 // ===========================================================================
+// dK / dV for head dim 256 with role-specialised waves.
+//
+// The same split with the whole head dim in every wave, so no partials are
+// exchanged: a workgroup owns 128 keys (four blocks of 32); P wave kb forms S
+// and P for key block kb, publishes P in fp32 and accumulates dV^T; dS wave kb
+// forms dP, reads P, forms dS and accumulates dK^T.  Two barriers per step:
+//   B1  the step's Q, dO, row data (and metadata) have landed.  P waves copy
+//       the next Q tile (and row data), form S, P and publish P; dS waves form
+//       dP and copy the next dO tile.
+//   B2  P published.  P waves: dV MFMAs; dS waves: dS, dK MFMAs.
+// ===========================================================================
+
+struct Roles256Cfg {
+  static constexpr int D = 256;
+  static constexpr int kNW = 8;
+  static constexpr int kNT = kNW * 64;
+  static constexpr int kBN = 128;  // keys per workgroup
+  static constexpr int kBM = 32;   // queries per step
+  static constexpr int kCPR = D / 8;
+  static constexpr int kNC = D / 16;
+  static constexpr int kNB = D / 32;
+  static constexpr int kTile = kBM * D * 2;
+  static constexpr int kLdsQ = 0;                   // [2 buf]
+  static constexpr int kLdsDo = kLdsQ + 2 * kTile;  // [2 buf]
+  static constexpr int kLdsP = kLdsDo + 2 * kTile;  // [kb][4][64 lanes][4 f32]
+  static constexpr int kLdsLd = kLdsP + 4 * 4096;   // [buf][lse x 32 | delta x 32] fp32
+  static constexpr int kLdsMeta = kLdsLd + 2 * 256; // [buf][vid x 32 | doc x 32] int32
+  static constexpr int kLdsRed = kLdsMeta + 2 * 256;
+  static constexpr int kLdsBytes = kLdsRed + 64;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+};
+
+template <bool META>
+struct Roles256Kernel {
+  using C = Roles256Cfg;
+  char G4_LDS* smem;
+  const BwdParams* a;
+  Seq sq;
+  int s, lane, wave, h32, kb;
+  int off, j0, my_j;
+  bool has_vid, has_doc, has_meta;
+  int my_vid, my_doc;
+  int grp, kvh, qt_lo, nqt;
+  int64_t tq;
+  RowReader<C::kCPR> rrd;
+  TrReader<C::kCPR> trd;
+  TileCopier<C::kCPR, C::kBM, 4> qcp, docp;  // Q by the P waves, dO by the dS waves
+  bf16x8 frag[C::kNC];  // K (P waves) or V (dS waves)
+  f32x16 acc[C::kNB];   // dV^T (P waves) or dK^T (dS waves)
+
+  __device__ __forceinline__ void coords(int it, int& qh, int& i0) const {
+    const int sh = __builtin_ctz(grp);
+    qh = kvh * grp + (it & (grp - 1));
+    i0 = (qt_lo + nqt - 1 - (it >> sh)) * C::kBM;
+  }
+  __device__ __forceinline__ void issue_do(int it, int buf) {
+    int qh, i0;
+    coords(it, qh, i0);
+    const __bf16* db =
+        a->dout + tok_off(sq, s, sq.qtok, i0, a->dol) + (int64_t)qh * a->dol.head_stride;
+    docp.issue_clamped(db, a->dol.token_stride, min(C::kBM, sq.lq - i0),
+                       smem + C::kLdsDo + buf * C::kTile);
+  }
+  __device__ __forceinline__ void issue_q(int it, int buf) {
+    int qh, i0;
+    coords(it, qh, i0);
+    const __bf16* qb = a->q + tok_off(sq, s, sq.qtok, i0, a->ql) + (int64_t)qh * a->ql.head_stride;
+    qcp.issue_clamped(qb, a->ql.token_stride, min(C::kBM, sq.lq - i0),
+                      smem + C::kLdsQ + buf * C::kTile);
+    const int i = min(i0 + (lane & 31), sq.lq - 1);
+    if (wave == 0) {
+      char G4_LDS* dst = smem + C::kLdsLd + buf * 256;
+      if (lane < 32)
+        g2l4(a->lse + lse_off(a->p, sq, s, qh, i), dst);
+      else
+        g2l4(a->delta + (int64_t)qh * tq + sq.qtok + i, dst);
+    } else if (wave == 1 && has_meta) {
+      char G4_LDS* dst = smem + C::kLdsMeta + buf * 256;
+      const int64_t kidx = sq.ktok + i + off;
+      if (lane < 32) {
+        if (has_vid) g2l4(a->p.vision_ids + kidx, dst);
+      } else {
+        if (has_doc) g2l4(a->p.document_ids + kidx, dst);
+      }
+    }
+  }
+  template <int M, int B>
+  __device__ __forceinline__ void acc_step(const char G4_LDS* t, const bf16x8 (&b)[2]) {
+    if constexpr (B < C::kNB) {
+      bf16x8 x = trd.template read<16 * M, 0, B>(t);
+      acc[B] = mfma32(x, b[M], acc[B]);
+      acc_step<M, B + 1>(t, b);
+    }
+  }
+  template <int CP>
+  __device__ __forceinline__ void row_step(const char G4_LDS* t, f32x16& part) const {
+    if constexpr (CP < C::kNC) {
+      bf16x8 x = rrd.template read<0, 0, CP>(t);
+      part = mfma32(x, frag[CP], part);
+      row_step<CP + 1>(t, part);
+    }
+  }
+  __device__ __forceinline__ char G4_LDS* pslot(int q4) const {
+    return smem + C::kLdsP + ((kb * 4 + q4) * 64 + lane) * 16;
+  }
+
+  // Values r of a lane are query rows 8 (r >> 2) + 4 h32 + (r & 3); lanes own keys.
+  __device__ __forceinline__ void step_p(int cur, int it, int nsteps) {
+    int qh, i0;
+    coords(it, qh, i0);
+    vm_wait<0>();
+    barrier_lds();  // B1
+    const char G4_LDS* qt = smem + C::kLdsQ + cur * C::kTile;
+    const char G4_LDS* dot = smem + C::kLdsDo + cur * C::kTile;
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 sv = f32x16{};
+    if (it + 1 < nsteps) issue_q(it + 1, cur ^ 1);
+    row_step<0>(qt, sv);
+    mfma_read_hint<C::kNC, 1, 1, 3>();
+    __builtin_amdgcn_sched_barrier(0);
+
+    const float* ld = (const float*)(smem + C::kLdsLd + cur * 256);
+    const bool full = !has_doc && (i0 + C::kBM <= sq.lq) && (j0 + C::kBN <= sq.lk) &&
+                      (j0 + C::kBN - 1 <= i0 + off) &&
+                      (a->p.window <= 0 || j0 > i0 + C::kBM - 1 + off - a->p.window);
+    bf16x8 pb[2];
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int il0 = 8 * r4 + 4 * h32;
+      const f32x4 lse4 = *(const f32x4*)(ld + il0);
+      i32x4 vq4 = {-1, -1, -1, -1}, dq4 = {0, 0, 0, 0};
+      if (has_meta && !full) {
+        const int* mt = (const int*)(smem + C::kLdsMeta + cur * 256);
+        vq4 = *(const i32x4*)(mt + il0);
+        dq4 = *(const i32x4*)(mt + 32 + il0);
+      }
+      f32x4 pv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float p = fast_exp2(sv[4 * r4 + e] * kLog2e - lse4[e] * kLog2e);
+        if (!full) {
+          const int i = i0 + il0 + e;
+          const int aq = i + off;
+          const bool in_w = a->p.window <= 0 || my_j > aq - a->p.window;
+          const bool causal = my_j <= aq;
+          const bool vis = has_vid & (vq4[e] >= 0) & (vq4[e] == my_vid);
+          const bool doc_ok = !has_doc | (dq4[e] == my_doc);
+          const bool ok = (i < sq.lq) & (my_j < sq.lk) & in_w & (causal | vis) & doc_ok;
+          p = ok ? p : 0.f;
+        }
+        pv[e] = p;
+        pb[r4 >> 1][4 * (r4 & 1) + e] = (__bf16)p;
+      }
+      *(f32x4 G4_LDS*)pslot(r4) = pv;
+    }
+    barrier_lds();  // B2
+
+    __builtin_amdgcn_sched_barrier(0);
+    acc_step<0, 0>(dot, pb);
+    acc_step<1, 0>(dot, pb);
+    mfma_read_hint<2 * C::kNB, 1, 2, 6>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  __device__ __forceinline__ void step_ds(int cur, int it, int nsteps) {
+    vm_wait<0>();
+    barrier_lds();  // B1
+    const char G4_LDS* qt = smem + C::kLdsQ + cur * C::kTile;
+    const char G4_LDS* dot = smem + C::kLdsDo + cur * C::kTile;
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 dp = f32x16{};
+    row_step<0>(dot, dp);
+    mfma_read_hint<C::kNC, 1, 1, 3>();
+    __builtin_amdgcn_sched_barrier(0);
+    if (it + 1 < nsteps) issue_do(it + 1, cur ^ 1);
+    barrier_lds();  // B2
+
+    const float* ld = (const float*)(smem + C::kLdsLd + cur * 256);
+    bf16x8 db[2];
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const f32x4 pv = *(const f32x4 G4_LDS*)pslot(r4);
+      const f32x4 del4 = *(const f32x4*)(ld + 32 + 8 * r4 + 4 * h32);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        db[r4 >> 1][4 * (r4 & 1) + e] = (__bf16)(pv[e] * (dp[4 * r4 + e] - del4[e]));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    acc_step<0, 0>(qt, db);
+    acc_step<1, 0>(qt, db);
+    mfma_read_hint<2 * C::kNB, 1, 2, 6>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  template <bool PWAVE>
+  __device__ __forceinline__ void run(int nsteps) {
+    const int jc = min(my_j, sq.lk - 1);
+    const __bf16* src = PWAVE ? a->k + tok_off(sq, s, sq.ktok, jc, a->kl) +
+                                    (int64_t)kvh * a->kl.head_stride
+                              : a->v + tok_off(sq, s, sq.ktok, jc, a->vl) +
+                                    (int64_t)kvh * a->vl.head_stride;
+    src += h32 * 8;
+#pragma unroll
+    for (int c = 0; c < C::kNC; ++c) frag[c] = ld_global16(src + c * 16);
+#pragma unroll
+    for (int b = 0; b < C::kNB; ++b) acc[b] = f32x16{};
+    for (int it = 0; it < nsteps; ++it) {
+      if constexpr (PWAVE)
+        step_p(it & 1, it, nsteps);
+      else
+        step_ds(it & 1, it, nsteps);
+    }
+    if (my_j >= sq.lk) return;
+    __bf16* dst = PWAVE ? a->dv + tok_off(sq, s, sq.ktok, my_j, a->dvl) +
+                              (int64_t)kvh * a->dvl.head_stride
+                        : a->dk + tok_off(sq, s, sq.ktok, my_j, a->dkl) +
+                              (int64_t)kvh * a->dkl.head_stride;
+#pragma unroll
+    for (int b = 0; b < C::kNB; ++b)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = b * 32 + 8 * r4 + 4 * h32;
+        const f32x16& x = acc[b];
+        *(bf16x4*)(dst + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
+                                     (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
+      }
+  }
+};
+
+template <bool META>
+__global__ void __launch_bounds__(Roles256Cfg::kNT, 1) dkdv_roles256_kernel(BwdParams a) {
+  using K = Roles256Kernel<META>;
+  using C = Roles256Cfg;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  K ker;
+  ker.smem = (char G4_LDS*)smem_raw;
+  ker.a = &a;
+  const g4_problem& p = a.p;
+  const int tid = threadIdx.x;
+  ker.lane = tid & 63;
+  ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool pwave = ker.wave < 4;
+  ker.kb = ker.wave & 3;
+  ker.h32 = ker.lane >> 5;
+
+  ker.grp = p.num_q_heads / p.num_kv_heads;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_kvh = a.num_seqs * a.ntiles;
+  ker.kvh = L / per_kvh;
+  const int rank = L % per_kvh;
+  ker.s = rank / a.ntiles;
+  const int kt = zigzag(rank % a.ntiles, a.ntiles);
+  ker.sq = resolve_seq(p, ker.s);
+  const Seq& sq = ker.sq;
+  ker.j0 = kt * C::kBN;
+  if (ker.j0 >= sq.lk) return;
+  ker.off = sq.lk - sq.lq;
+  ker.tq = q_stream_tokens_dev(p);
+  ker.has_vid = META && p.vision_ids != nullptr && p.bidirectional_vision;
+  ker.has_doc = META && p.document_ids != nullptr;
+  ker.has_meta = ker.has_vid || ker.has_doc;
+  const int j_last = min(ker.j0 + C::kBN, sq.lk) - 1;
+  ker.my_j = ker.j0 + ker.kb * 32 + (ker.lane & 31);
+
+  int span_min = 0x7fffffff;
+  if (ker.has_vid) {
+    int* red = (int*)(smem_raw + C::kLdsRed);
+    int v = 0x7fffffff;
+    for (int t = tid; t < C::kBN; t += C::kNT) {
+      int j = ker.j0 + t;
+      if (j < sq.lk) v = min(v, a.span_lo[sq.ktok + j]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+    if (ker.lane == 0) red[ker.wave] = v;
+    barrier_lds();
+#pragma unroll
+    for (int w = 0; w < C::kNW; ++w) span_min = min(span_min, red[w]);
+  }
+  int ilo, ihi;
+  key_tile_query_range(ker.j0, j_last, sq.lq, ker.off, p.window, span_min, ilo, ihi);
+  ker.qt_lo = ilo / C::kBM;
+  ker.nqt = ihi > ilo ? (ihi + C::kBM - 1) / C::kBM - ker.qt_lo : 0;
+  if (ker.has_doc && ker.nqt > 0 &&
+      doc_uniform<C::kNW>(p.document_ids, sq.ktok, sq.lk,
+                          min(ker.j0, ker.qt_lo * C::kBM + ker.off),
+                          max(j_last + 1, (ker.qt_lo + ker.nqt) * C::kBM + ker.off), tid,
+                          ker.lane, ker.wave, (int*)(smem_raw + C::kLdsRed))) {
+    ker.has_doc = false;
+    ker.has_meta = ker.has_vid;
+  }
+  const int nsteps = ker.nqt * ker.grp;
+  const int jc = min(ker.my_j, sq.lk - 1);
+  ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + jc] : -1;
+  ker.my_doc = ker.has_doc ? p.document_ids[sq.ktok + jc] : 0;
+
+  ker.rrd.init(ker.lane, 0);
+  ker.trd.init(ker.lane, 0);
+  ker.qcp.init(a.ql.token_stride, ker.wave & 3, ker.lane);
+  ker.docp.init(a.dol.token_stride, ker.wave & 3, ker.lane);
+  if (nsteps > 0) {
+    if (pwave)
+      ker.issue_q(0, 0);
+    else
+      ker.issue_do(0, 0);
+  }
+  // Both roles run nsteps steps of two barriers each.
+  if (pwave)
+    ker.template run<true>(nsteps);
+  else
+    ker.template run<false>(nsteps);
+}
+
+// ===========================================================================
 // dQ for head dim 512 with role-specialised waves.
 //
 // A workgroup owns 64 queries (two groups of 32) of one query head and walks
@@ -710,11 +1026,16 @@ hipError_t launch_dq_roles(const BwdParams& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_dkdv_roles(const BwdParams& a, hipStream_t stream) {
-  using C = RolesCfg;
+template <int D>
+hipError_t launch_dkdv_roles_d(const BwdParams& a, hipStream_t stream) {
+  using C = std::conditional_t<D == 512, RolesCfg, Roles256Cfg>;
   const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
                     a.p.document_ids != nullptr;
-  auto kern = meta ? dkdv_roles_kernel<true> : dkdv_roles_kernel<false>;
+  void (*kern)(BwdParams);
+  if constexpr (D == 512)
+    kern = meta ? dkdv_roles_kernel<true> : dkdv_roles_kernel<false>;
+  else
+    kern = meta ? dkdv_roles256_kernel<true> : dkdv_roles256_kernel<false>;
   static bool done[2] = {false, false};
   if (!done[meta]) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
@@ -728,6 +1049,12 @@ hipError_t launch_dkdv_roles(const BwdParams& a, hipStream_t stream) {
   if (nblocks <= 0) return hipSuccess;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();
+}
+
+hipError_t launch_dkdv_roles(const BwdParams& a, hipStream_t stream) {
+  if (a.p.head_dim == 512) return launch_dkdv_roles_d<512>(a, stream);
+  if (a.p.head_dim == 256) return launch_dkdv_roles_d<256>(a, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace g4

@@ -818,9 +818,8 @@ hipError_t launch_dq_cfg(const BwdParams& a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_bwd_dkdv(const BwdParams& a, hipStream_t stream) {
-  if (a.p.head_dim == 256) return launch_dkdv_cfg<256, 1, 4, true, true, 1>(a, stream);
-  // d512: role-specialised waves (a dV role and a dK role per SIMD).
-  if (a.p.head_dim == 512) return launch_dkdv_roles(a, stream);
+  // Role-specialised waves (a dV role and a dK role per SIMD).
+  if (a.p.head_dim == 256 || a.p.head_dim == 512) return launch_dkdv_roles(a, stream);
   return hipErrorInvalidValue;
 }
 
