@@ -1004,13 +1004,288 @@ __global__ void __launch_bounds__(DqRolesCfg::kNT, 1) dq_roles_kernel(BwdParams 
   }
 }
 
+// ===========================================================================
+// dQ for head dim 256 with role-specialised waves.
+//
+// A workgroup owns 128 queries (four groups of 32) of one query head and walks
+// the 32-key tiles its range admits.  Per query group an S wave (Q fragments)
+// forms S^T and P, a dP wave (dO fragments) forms dP^T; each publishes its
+// tile in fp32, reads the other's and forms the same dS, and accumulates dQ^T
+// over one head-dim half.  Per key tile two barriers:
+//   B1  K(t), V(t) and key metadata have landed; K(t+1) goes out.
+//   B2  P and dP published; V(t+1) goes out (V is read only before B2).
+// ===========================================================================
+
+struct DqRoles256Cfg {
+  static constexpr int D = 256;
+  static constexpr int kNW = 8;
+  static constexpr int kNT = kNW * 64;
+  static constexpr int kBM = 128;  // queries per workgroup
+  static constexpr int kBN = 32;   // keys per tile
+  static constexpr int kDQ = 128;  // head-dim half of a dQ accumulator
+  static constexpr int kCPR = D / 8;
+  static constexpr int kNC = D / 16;
+  static constexpr int kNB = kDQ / 32;
+  static constexpr int kTile = kBN * D * 2;
+  static constexpr int kLdsK = 0;                  // [2 buf] K tiles
+  static constexpr int kLdsV = kLdsK + 2 * kTile;  // one V tile
+  // Published tiles: [slot = 2 qg + role][4][64 lanes][4 f32] (P, dP).
+  static constexpr int kLdsX = kLdsV + kTile;
+  static constexpr int kLdsMeta = kLdsX + 8 * 4096;  // [buf][vid x 64 | doc x 64] int32
+  static constexpr int kLdsRed = kLdsMeta + 2 * 512;
+  static constexpr int kLdsBytes = kLdsRed + 64;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+};
+
+template <bool META>
+struct DqRoles256Kernel {
+  using C = DqRoles256Cfg;
+  char G4_LDS* smem;
+  const BwdParams* a;
+  Seq sq;
+  int lane, wave, role, qg, h32;
+  int my_a, my_vid, my_doc, a0;
+  bool has_vid, has_doc, has_meta, q_valid;
+  float my_lse2, my_delta;
+  const __bf16* kbase;
+  const __bf16* vbase;
+  int64_t kstride, vstride;
+  RowReader<C::kCPR> rrd;
+  TrReader<C::kCPR> trd;
+  TileCopier<C::kCPR, C::kBN, C::kNW> kcp, vcp;
+  bf16x8 frag[C::kNC];  // Q (S waves) or dO (dP waves) fragments
+  f32x16 acc[C::kNB];   // dQ^T over this wave's head-dim half
+
+  __device__ __forceinline__ void issue_k(int row0, int buf) {
+    kcp.issue_clamped(kbase + row0 * kstride, kstride, min(C::kBN, sq.lk - row0),
+                      smem + C::kLdsK + buf * C::kTile);
+    if (has_meta && wave == 0)
+      issue_key_meta(a->p, sq, row0, smem + C::kLdsMeta + buf * 512, lane, has_vid, has_doc);
+  }
+  __device__ __forceinline__ void issue_v(int row0) {
+    vcp.issue_clamped(vbase + row0 * vstride, vstride, min(C::kBN, sq.lk - row0),
+                      smem + C::kLdsV);
+  }
+  __device__ __forceinline__ char G4_LDS* xslot(int sl, int q4) const {
+    return smem + C::kLdsX + ((sl * 4 + q4) * 64 + lane) * 16;
+  }
+  template <int CP>
+  __device__ __forceinline__ void part_step(const char G4_LDS* t, f32x16& part) const {
+    if constexpr (CP < C::kNC) {
+      bf16x8 x = rrd.template read<0, 0, CP>(t);
+      part = mfma32(x, frag[CP], part);
+      part_step<CP + 1>(t, part);
+    }
+  }
+  template <int HK, int B>
+  __device__ __forceinline__ void dq_step(const char G4_LDS* kt, const bf16x8& ds) {
+    if constexpr (B < C::kNB) {
+      bf16x8 x = trd.template read<16 * HK, 0, B>(kt);
+      acc[B] = mfma32(x, ds, acc[B]);
+      dq_step<HK, B + 1>(kt, ds);
+    }
+  }
+
+  // Rows of the tiles are keys 8 (r >> 2) + 4 h32 + (r & 3); lanes own queries.
+  __device__ __forceinline__ void step(int cur, int it, int ntiles, int t_first) {
+    const int kb0 = (t_first + it) * C::kBN;
+    vm_wait<0>();
+    barrier_lds();  // B1
+    const char G4_LDS* kt = smem + C::kLdsK + cur * C::kTile;
+    const char G4_LDS* vt = smem + C::kLdsV;
+
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 part = f32x16{};
+    if (it + 1 < ntiles) issue_k(kb0 + C::kBN, cur ^ 1);
+    part_step<0>(role == 0 ? kt : vt, part);
+    mfma_read_hint<C::kNC, 1, 1, 3>();
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (role == 0) {
+      // S -> P (masked), in place.
+      const bool full = !has_doc && (kb0 + C::kBN <= sq.lk) && (kb0 + C::kBN - 1 <= a0) &&
+                        (a->p.window <= 0 || kb0 > a0 + C::kBM - 1 - a->p.window);
+      const int lo_w = a->p.window > 0 ? my_a - a->p.window + 1 : -0x40000000;
+      const int hi_c = min(my_a, sq.lk - 1);
+      const int* km = (const int*)(smem + C::kLdsMeta + cur * 512);
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int jl0 = 8 * r4 + 4 * h32;
+        i32x4 vk = {-1, -1, -1, -1}, dk = {0, 0, 0, 0};
+        if (has_meta && !full) {
+          vk = *(const i32x4*)(km + jl0);
+          dk = *(const i32x4*)(km + 64 + jl0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = r4 * 4 + e;
+          float p = fast_exp2(part[r] * kLog2e - my_lse2);
+          if (!full) {
+            const int j = kb0 + jl0 + e;
+            const bool in_w = j >= lo_w;
+            const bool causal = in_w & (j <= hi_c);
+            const bool vis = has_vid & (my_vid >= 0) & (vk[e] == my_vid) & in_w & (j < sq.lk);
+            const bool doc_ok = !has_doc | (dk[e] == my_doc);
+            p = ((causal | vis) & doc_ok & q_valid) ? p : 0.f;
+          }
+          part[r] = p;
+        }
+      }
+    }
+    const int own = 2 * qg + role;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+      *(f32x4 G4_LDS*)xslot(own, q4) =
+          f32x4{part[4 * q4], part[4 * q4 + 1], part[4 * q4 + 2], part[4 * q4 + 3]};
+    barrier_lds();  // B2
+    if (it + 1 < ntiles) issue_v(kb0 + C::kBN);
+
+    // dS = P (dP - delta) from the same fp32 values in both waves of the group.
+    bf16x8 dsb[2];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const f32x4 other = *(const f32x4 G4_LDS*)xslot(own ^ 1, q4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * q4 + e;
+        const float pp = role == 0 ? part[r] : other[e];
+        const float dp = role == 0 ? other[e] : part[r];
+        dsb[r >> 3][r & 7] = (__bf16)(pp * (dp - my_delta));
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    dq_step<0, 0>(kt, dsb[0]);
+    dq_step<1, 0>(kt, dsb[1]);
+    mfma_read_hint<2 * C::kNB, 1, 2, 4>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+};
+
+template <bool META>
+__global__ void __launch_bounds__(DqRoles256Cfg::kNT, 1) dq_roles256_kernel(BwdParams a) {
+  using K = DqRoles256Kernel<META>;
+  using C = DqRoles256Cfg;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  K ker;
+  ker.smem = (char G4_LDS*)smem_raw;
+  ker.a = &a;
+  const g4_problem& p = a.p;
+  const int tid = threadIdx.x;
+  ker.lane = tid & 63;
+  ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  ker.role = ker.wave >> 2;
+  ker.qg = ker.wave & 3;
+  ker.h32 = ker.lane >> 5;
+  const int l32 = ker.lane & 31;
+
+  const int grp = p.num_q_heads / p.num_kv_heads;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_kvh = a.num_seqs * a.ntiles * grp;
+  const int kvh = L / per_kvh;
+  const int rem = L % per_kvh;
+  const int rank = rem / grp;
+  const int qh = kvh * grp + rem % grp;
+  const int s = rank / a.ntiles;
+  const int qt = zigzag(rank % a.ntiles, a.ntiles);
+  ker.sq = resolve_seq(p, s);
+  const Seq& sq = ker.sq;
+  const int i0 = qt * C::kBM;
+  if (i0 >= sq.lq) return;
+  const int off = sq.lk - sq.lq;
+  ker.a0 = i0 + off;
+  const int a_last_valid = min(i0 + C::kBM, sq.lq) - 1 + off;
+  ker.has_vid = META && p.vision_ids != nullptr && p.bidirectional_vision;
+  ker.has_doc = META && p.document_ids != nullptr;
+  ker.has_meta = ker.has_vid || ker.has_doc;
+
+  int span_max = -1;
+  if (ker.has_vid) {
+    int* red = (int*)(smem_raw + C::kLdsRed);
+    int v = -1;
+    for (int t = tid; t < C::kBM; t += C::kNT) {
+      int i = i0 + t;
+      if (i < sq.lq) v = max(v, a.span_hi[sq.ktok + i + off]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+    if (ker.lane == 0) red[ker.wave] = v;
+    barrier_lds();
+#pragma unroll
+    for (int w = 0; w < C::kNW; ++w) span_max = max(span_max, red[w]);
+  }
+  int klo, khi;
+  query_tile_key_range(ker.a0, a_last_valid, sq.lk, p.window, span_max, klo, khi);
+  const int t_first = klo / C::kBN;
+  const int ntiles = (khi + C::kBN - 1) / C::kBN - t_first;
+  if (ker.has_doc &&
+      doc_uniform<C::kNW>(p.document_ids, sq.ktok, sq.lk, min(klo / 64 * 64, ker.a0),
+                          max((khi + 63) / 64 * 64, a_last_valid + 1), tid, ker.lane,
+                          ker.wave, (int*)(smem_raw + C::kLdsRed))) {
+    ker.has_doc = false;
+    ker.has_meta = ker.has_vid;
+  }
+
+  ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
+  ker.vbase = a.v + tok_off(sq, s, sq.ktok, 0, a.vl) + (int64_t)kvh * a.vl.head_stride;
+  ker.kstride = a.kl.token_stride;
+  ker.vstride = a.vl.token_stride;
+  ker.rrd.init(ker.lane, 0);
+  ker.trd.init(ker.lane, ker.role * C::kDQ * 2);
+  ker.kcp.init(ker.kstride, ker.wave, ker.lane);
+  ker.vcp.init(ker.vstride, ker.wave, ker.lane);
+
+  const int my_i = i0 + ker.qg * 32 + l32;
+  ker.my_a = my_i + off;
+  ker.q_valid = my_i < sq.lq;
+  const int ic = min(my_i, sq.lq - 1);
+  {
+    const __bf16* row =
+        ker.role == 0
+            ? a.q + tok_off(sq, s, sq.qtok, ic, a.ql) + (int64_t)qh * a.ql.head_stride
+            : a.dout + tok_off(sq, s, sq.qtok, ic, a.dol) + (int64_t)qh * a.dol.head_stride;
+    row += ker.h32 * 8;
+#pragma unroll
+    for (int c = 0; c < C::kNC; ++c) ker.frag[c] = ld_global16(row + c * 16);
+  }
+  ker.my_lse2 = a.lse[lse_off(p, sq, s, qh, ic)] * kLog2e;
+  ker.my_delta = a.delta[(int64_t)qh * q_stream_tokens_dev(p) + sq.qtok + ic];
+  ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + ic + off] : -1;
+  ker.my_doc = ker.has_doc ? p.document_ids[sq.ktok + ic + off] : 0;
+#pragma unroll
+  for (int b = 0; b < C::kNB; ++b) ker.acc[b] = f32x16{};
+
+  if (ntiles > 0) {
+    ker.issue_k(t_first * C::kBN, 0);
+    ker.issue_v(t_first * C::kBN);
+  }
+  for (int it = 0; it < ntiles; ++it) ker.step(it & 1, it, ntiles, t_first);
+
+  if (ker.q_valid) {
+    __bf16* row = a.dq + tok_off(sq, s, sq.qtok, my_i, a.dql) + (int64_t)qh * a.dql.head_stride;
+#pragma unroll
+    for (int b = 0; b < C::kNB; ++b)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = ker.role * C::kDQ + b * 32 + 8 * r4 + 4 * ker.h32;
+        const f32x16& x = ker.acc[b];
+        *(bf16x4*)(row + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
+                                     (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
+      }
+  }
+}
+
 }  // namespace
 
-hipError_t launch_dq_roles(const BwdParams& a, hipStream_t stream) {
-  using C = DqRolesCfg;
+template <int D>
+hipError_t launch_dq_roles_d(const BwdParams& a, hipStream_t stream) {
+  using C = std::conditional_t<D == 512, DqRolesCfg, DqRoles256Cfg>;
   const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
                     a.p.document_ids != nullptr;
-  auto kern = meta ? dq_roles_kernel<true> : dq_roles_kernel<false>;
+  void (*kern)(BwdParams);
+  if constexpr (D == 512)
+    kern = meta ? dq_roles_kernel<true> : dq_roles_kernel<false>;
+  else
+    kern = meta ? dq_roles256_kernel<true> : dq_roles256_kernel<false>;
   static bool done[2] = {false, false};
   if (!done[meta]) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
@@ -1024,6 +1299,12 @@ hipError_t launch_dq_roles(const BwdParams& a, hipStream_t stream) {
   if (nblocks <= 0) return hipSuccess;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();
+}
+
+hipError_t launch_dq_roles(const BwdParams& a, hipStream_t stream) {
+  if (a.p.head_dim == 512) return launch_dq_roles_d<512>(a, stream);
+  if (a.p.head_dim == 256) return launch_dq_roles_d<256>(a, stream);
+  return hipErrorInvalidValue;
 }
 
 template <int D>

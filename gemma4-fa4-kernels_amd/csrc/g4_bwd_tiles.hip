@@ -824,9 +824,8 @@ hipError_t launch_bwd_dkdv(const BwdParams& a, hipStream_t stream) {
 }
 
 hipError_t launch_bwd_dq(const BwdParams& a, hipStream_t stream) {
-  if (a.p.head_dim == 256) return launch_dq_cfg<256, 64, 1, 4, true>(a, stream);
-  // d512: role-specialised waves (S waves and dP waves per SIMD).
-  if (a.p.head_dim == 512) return launch_dq_roles(a, stream);
+  // Role-specialised waves (S waves and dP waves per SIMD).
+  if (a.p.head_dim == 256 || a.p.head_dim == 512) return launch_dq_roles(a, stream);
   return hipErrorInvalidValue;
 }
 
