@@ -1,4 +1,17 @@
-// dK / dV for head dim 512 on gfx950 with role-specialised waves.
+// Backward tile kernels for gfx950 (dK/dV and dQ, head dims 256 and 512), all
+// with role-specialised waves: eight waves per workgroup, two per SIMD, each
+// wave holding one operand fragment set and one accumulator, so a SIMD always
+// has a second wave whose MFMAs overlap the first one's VALU and LDS work.
+// Both recompute P = exp2(S log2e - LSE log2e) from the saved fp32 LSE and use
+// delta = rowsum(O dO) - dLSE from the pre-pass (g4_bwd.hip): dS = P (dP -
+// delta), S = Q K^T, dP = dO V^T, softmax scale 1.0.  P and dS are rounded to
+// bf16 before they feed the dV / dK / dQ products.  No atomics: each output
+// element is written by one wave, so results repeat bitwise.  dK/dV is
+// key-tile major (the GQA group's query heads are reduced on chip); dQ is
+// query-tile major.
+//
+// ---------------------------------------------------------------------------
+// dK / dV for head dim 512.
 //
 // A workgroup owns 64 keys (two blocks of 32) of one KV head and runs eight
 // waves, two per SIMD.  Four P waves (one per key block and head-dim half)
@@ -1301,7 +1314,7 @@ hipError_t launch_dq_roles_d(const BwdParams& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_dq_roles(const BwdParams& a, hipStream_t stream) {
+hipError_t launch_bwd_dq(const BwdParams& a, hipStream_t stream) {
   if (a.p.head_dim == 512) return launch_dq_roles_d<512>(a, stream);
   if (a.p.head_dim == 256) return launch_dq_roles_d<256>(a, stream);
   return hipErrorInvalidValue;
@@ -1332,7 +1345,7 @@ hipError_t launch_dkdv_roles_d(const BwdParams& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_dkdv_roles(const BwdParams& a, hipStream_t stream) {
+hipError_t launch_bwd_dkdv(const BwdParams& a, hipStream_t stream) {
   if (a.p.head_dim == 512) return launch_dkdv_roles_d<512>(a, stream);
   if (a.p.head_dim == 256) return launch_dkdv_roles_d<256>(a, stream);
   return hipErrorInvalidValue;

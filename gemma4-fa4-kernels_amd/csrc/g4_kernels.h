@@ -56,8 +56,6 @@ void span_arrays(const g4_problem& p, void* ws, const int** lo, const int** hi);
 hipError_t launch_fwd(const FwdParams& a, hipStream_t stream);
 hipError_t launch_bwd_delta(const BwdParams& a, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const BwdParams& a, hipStream_t stream);
-hipError_t launch_dkdv_roles(const BwdParams& a, hipStream_t stream);
-hipError_t launch_dq_roles(const BwdParams& a, hipStream_t stream);
 hipError_t launch_bwd_dq(const BwdParams& a, hipStream_t stream);
 hipError_t launch_mask(const g4_problem& p, uint8_t* out, const int* span_lo, const int* span_hi,
                        hipStream_t stream);
