@@ -47,6 +47,10 @@ __device__ __forceinline__ void issue_meta(const g4_problem& p, const Seq& sq, i
   if (doc) g2l4(p.document_ids + idx, dst + 256);
 }
 
+// Largest score excess (log2 units) over a row's running maximum that the
+// online softmax absorbs without rescaling the O accumulators.
+constexpr float kRescaleLog2 = 8.0f;
+
 // META: key metadata kinds compiled in (bit 0 vision IDs, bit 1 document IDs).
 template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, int META, int OCC = 1>
 struct FwdKernel {
@@ -217,7 +221,11 @@ struct FwdKernel {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
     mx = fmaxf(mx, wave_xor32(mx));
-    const float m_new = fmaxf(m_run, mx);
+    // The running maximum only moves when a row's scores exceed it by more
+    // than kRescaleLog2 (P <= 2^kRescaleLog2 meanwhile, exact in fp32 and in
+    // bf16 range), so the O accumulators are rescaled rarely after the first
+    // admitted tile instead of on most tiles.
+    const float m_new = mx > m_run + kRescaleLog2 ? mx : m_run;
     const float m_use = m_new == kNegInf ? 0.f : m_new;
     const float alpha = fast_exp2(m_run - m_use);
     float rs = 0.f;
