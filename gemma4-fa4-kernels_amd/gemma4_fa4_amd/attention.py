@@ -183,8 +183,13 @@ def _prepare_vision_block_ids(vision_block_ids: torch.Tensor, q: torch.Tensor) -
 
 
 def _cumulative_lengths(cu_q, cu_k, q, k, *, label: str):
-    q_vals = [int(x) for x in cu_q.detach().cpu().tolist()]
-    k_vals = [int(x) for x in cu_k.detach().cpu().tolist()]
+    # One device-to-host copy (and stream sync) for both arrays.
+    if cu_q.data_ptr() == cu_k.data_ptr() and cu_q.shape == cu_k.shape:
+        q_vals = cu_q.detach().cpu().tolist()
+        k_vals = q_vals
+    else:
+        both = torch.cat((cu_q.detach(), cu_k.detach())).cpu().tolist()
+        q_vals, k_vals = both[: cu_q.numel()], both[cu_q.numel():]
     if q_vals[0] != 0 or k_vals[0] != 0:
         raise ValueError(f"{label} cumulative arrays must start at zero")
     if q_vals[-1] != q.shape[0] or k_vals[-1] != k.shape[0]:
