@@ -94,12 +94,36 @@ int* raise_flags_ptr(const g4_problem& p, void* ws) {
 float* delta_ptr(const g4_problem& p, void* ws) {
   return (float*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p));
 }
+__bf16* ds_ptr(const g4_problem& p, void* ws) {
+  if (!g4::ds_bytes(p)) return nullptr;
+  return (__bf16*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) +
+                   g4::delta_bytes(p));
+}
 
 }  // namespace
 
 namespace g4 {
 size_t delta_bytes(const g4_problem& p) {
   return align256((size_t)q_stream_tokens(p) * p.num_q_heads * 4);
+}
+// dS tiles for the head-dim 512 causal backward: the dK/dV kernel writes each
+// step's dS (bf16) and the dQ stage is then a plain product dQ^T = K^T dS^T
+// instead of recomputing S and dP.  Used for text-causal problems (no window,
+// no bidirectional vision: every tile pair lies in the causal triangle of its
+// sequence) while the buffer stays within 16 GiB.
+void ds_geometry(const g4_problem& p, int* rows, int* cols) {
+  const int64_t r = p.cu_seqlens_q ? p.total_q / 32 + p.num_seqs
+                                   : (int64_t)p.num_seqs * ((p.seqlen_q + 31) / 32);
+  *rows = (int)r;
+  *cols = (p.seqlen_k + 63) / 64;
+}
+size_t ds_bytes(const g4_problem& p) {
+  if (p.head_dim != 512 || p.window != 0 || (p.vision_ids != nullptr && p.bidirectional_vision))
+    return 0;
+  int rows, cols;
+  ds_geometry(p, &rows, &cols);
+  const size_t b = (size_t)rows * cols * p.num_q_heads * 4096;
+  return b <= (size_t(16) << 30) ? b : 0;
 }
 // One int per (sequence, 32-query group, query head) for the head-dim 512
 // forward's second pass.
@@ -118,7 +142,7 @@ const char* g4_last_error(void) { return g_last_error.c_str(); }
 size_t g4_workspace_bytes(const g4_problem* p, int phase) {
   if (check_problem(p) != G4_OK) return 0;
   size_t b = align256(g4::spans_bytes(*p)) + g4::raise_flags_bytes(*p);
-  if (phase == 1) b += g4::delta_bytes(*p);
+  if (phase == 1) b += g4::delta_bytes(*p) + g4::ds_bytes(*p);
   return b;
 }
 
@@ -167,6 +191,8 @@ static int fill_bwd(g4::BwdParams& a, const g4_problem* p, const void* q, g4_lay
   a.vl = vl;
   a.num_seqs = p->num_seqs;
   a.delta = delta_ptr(*p, ws);
+  a.ds = ds_ptr(*p, ws);
+  g4::ds_geometry(*p, &a.ds_rows, &a.ds_cols);
   g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);
   return G4_OK;
 }

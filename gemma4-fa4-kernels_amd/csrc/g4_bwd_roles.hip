@@ -84,6 +84,7 @@ struct RolesKernel {
   int my_vid, my_doc;
   int grp, kvh, qt_lo, nqt;
   int64_t tq;
+  int64_t ds_row0;  // dS tile row of this sequence's first query tile
   RowReader<C::kCPR> rrd;
   TrReader<C::kCPR> trd;
   TileCopier<C::kCPR, C::kBM, 4> qcp, docp;  // Q by the P waves, dO by the dS waves
@@ -236,6 +237,8 @@ struct RolesKernel {
   }
 
   __device__ __forceinline__ void step_ds(int cur, int it, int nsteps) {
+    int qh, i0;
+    coords(it, qh, i0);
     vm_wait<0>();
     barrier_lds();  // B1
     const char G4_LDS* qt = smem + C::kLdsQ + cur * C::kTile;
@@ -280,6 +283,20 @@ struct RolesKernel {
           db[m][4 * q4 + e] = (__bf16)(pv[e] * (dp[r] - del4[e]));
         }
       }
+    if (a->ds != nullptr && dh == 0) {
+      // dS tile [64 keys][32 queries]: this lane's key row, four runs of four
+      // queries (rows 8 (r >> 2) + 4 h32 + (r & 3) of the accumulator layout).
+      char* row = (char*)a->ds +
+                  (((int64_t)qh * a->ds_cols + j0 / C::kBN) * a->ds_rows + ds_row0 + i0 / 32) *
+                      4096 +
+                  (kb * 32 + (lane & 31)) * 64;
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int q4 = 0; q4 < 2; ++q4)
+          *(bf16x4*)(row + (8 * (2 * m + q4) + 4 * h32) * 2) =
+              bf16x4{db[m][4 * q4], db[m][4 * q4 + 1], db[m][4 * q4 + 2], db[m][4 * q4 + 3]};
+    }
     __builtin_amdgcn_sched_barrier(0);
     acc_step<0, 0>(qt, db);
     acc_step<1, 0>(qt, db);
@@ -392,6 +409,7 @@ __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams 
     ker.has_meta = ker.has_vid;
   }
   const int nsteps = ker.nqt * ker.grp;
+  ker.ds_row0 = sq.packed ? sq.qtok / 32 + ker.s : (int64_t)ker.s * ((p.seqlen_q + 31) / 32);
   const int jc = min(ker.my_j, sq.lk - 1);
   ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + jc] : -1;
   ker.my_doc = ker.has_doc ? p.document_ids[sq.ktok + jc] : 0;
@@ -1287,7 +1305,216 @@ __global__ void __launch_bounds__(DqRoles256Cfg::kNT, 1) dq_roles256_kernel(BwdP
   }
 }
 
+// ===========================================================================
+// dQ for head dim 512 from the dS tiles the dK/dV kernel wrote:
+// dQ^T = K^T dS^T, no recomputation of S or dP.
+//
+// A workgroup owns 128 queries (four 32-query tile rows) of one query head and
+// walks the 64-key tiles of their causal range; eight waves, wave w holding
+// dQ^T for two rows (2 (w >> 2) + {0, 1}) over head-dim quarter w & 3.  Both
+// operands come from transposing LDS reads with the same reduction-dim order:
+// K^T from the swizzled K tile, dS^T from the plain [64 keys][32 queries]
+// tile.  A row's tiles past its own causal range were never written and are
+// skipped.  One barrier per key tile (copies one tile ahead).
+// ===========================================================================
+
+struct DqDsCfg {
+  static constexpr int D = 512;
+  static constexpr int kNW = 8;
+  static constexpr int kNT = kNW * 64;
+  static constexpr int kBM = 128;  // queries per workgroup (four tile rows)
+  static constexpr int kBN = 64;   // keys per tile
+  static constexpr int kCPR = D / 8;
+  static constexpr int kKTile = kBN * D * 2;
+  static constexpr int kLdsK = 0;                    // [2 buf] K tiles
+  static constexpr int kLdsDs = 2 * kKTile;          // [2 buf][4 rows] dS tiles
+  static constexpr int kLdsBytes = kLdsDs + 2 * 4 * 4096;
+  static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+};
+
+// Transposing reads of a plain (unswizzled) tile of 64-byte rows (32 bf16
+// columns): the MFMA operand [32 columns x 16 rows] with the same row order as
+// TrReader's.
+struct PlainTrReader {
+  int base[2];
+  __device__ __forceinline__ void init(int lane) {
+    const int g = lane >> 4, sl = lane & 15;
+    const int rl = 4 * (g >> 1) + (sl >> 2);
+    const int lb = 2 * (g & 1) + ((sl >> 1) & 1);
+    const int half = (sl & 1) * 8;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) base[e] = (rl + 8 * e) * 64 + 16 * lb + half;
+  }
+  template <int ROW0>
+  __device__ __forceinline__ bf16x8 read(const char G4_LDS* tile) const {
+    bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (bf16x4 G4_LDS*)(tile + base[0] + ROW0 * 64));
+    bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (bf16x4 G4_LDS*)(tile + base[1] + ROW0 * 64));
+    return cat4(lo, hi);
+  }
+};
+
+struct DqDsKernel {
+  using C = DqDsCfg;
+  char G4_LDS* smem;
+  const BwdParams* a;
+  Seq sq;
+  int lane, wave, h32, dquart, qpair;
+  // Last key tile (-1: row past the sequence) of this wave's two tile rows and
+  // of the row whose dS tiles this wave copies.
+  int ktm0, ktm1, ktm_copy;
+  const __bf16* kbase;
+  int64_t kstride;
+  const char* ds_col0;  // dS tile of key tile 0, first tile row of this workgroup
+  int64_t ds_col_stride;
+  TrReader<C::kCPR> trk;
+  PlainTrReader trs;
+  TileCopier<C::kCPR, C::kBN, C::kNW> kcp;
+  f32x16 acc[2][4];
+
+  __device__ __forceinline__ void issue(int kt, int buf) {
+    const int row0 = kt * C::kBN;
+    kcp.issue_clamped(kbase + row0 * kstride, kstride, min(C::kBN, sq.lk - row0),
+                      smem + C::kLdsK + buf * C::kKTile);
+    // dS: four 4 KB tiles, two 1 KB chunks per wave.
+    const int g = wave >> 1;
+    if (kt <= ktm_copy) {
+      const char* src = ds_col0 + kt * ds_col_stride + g * 4096;
+      char G4_LDS* dst = smem + C::kLdsDs + (buf * 4 + g) * 4096;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int chunk = (wave & 1) * 2 + c;
+        g2l16(src + chunk * 1024 + lane * 16, dst + chunk * 1024);
+      }
+    }
+  }
+
+  template <int KS>
+  __device__ __forceinline__ void kstep(const char G4_LDS* kt_tile, const char G4_LDS* ds0,
+                                        const char G4_LDS* ds1, bool v0, bool v1) {
+    const bf16x8 ak[4] = {trk.template read<16 * KS, 0, 0>(kt_tile),
+                          trk.template read<16 * KS, 0, 1>(kt_tile),
+                          trk.template read<16 * KS, 0, 2>(kt_tile),
+                          trk.template read<16 * KS, 0, 3>(kt_tile)};
+    if (v0) {
+      const bf16x8 bs = trs.template read<16 * KS>(ds0);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[0][b] = mfma32(ak[b], bs, acc[0][b]);
+    }
+    if (v1) {
+      const bf16x8 bs = trs.template read<16 * KS>(ds1);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[1][b] = mfma32(ak[b], bs, acc[1][b]);
+    }
+  }
+};
+
+__global__ void __launch_bounds__(DqDsCfg::kNT, 1) dq_ds_kernel(BwdParams a) {
+  using C = DqDsCfg;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  DqDsKernel ker;
+  ker.smem = (char G4_LDS*)smem_raw;
+  ker.a = &a;
+  const g4_problem& p = a.p;
+  const int tid = threadIdx.x;
+  ker.lane = tid & 63;
+  ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  ker.h32 = ker.lane >> 5;
+  ker.dquart = ker.wave & 3;
+  ker.qpair = ker.wave >> 2;
+  const int l32 = ker.lane & 31;
+
+  const int grp = p.num_q_heads / p.num_kv_heads;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_kvh = a.num_seqs * a.ntiles * grp;
+  const int kvh = L / per_kvh;
+  const int rem = L % per_kvh;
+  const int rank = rem / grp;
+  const int qh = kvh * grp + rem % grp;
+  const int s = rank / a.ntiles;
+  const int qt = zigzag(rank % a.ntiles, a.ntiles);
+  ker.sq = resolve_seq(p, s);
+  const Seq& sq = ker.sq;
+  const int i0 = qt * C::kBM;
+  if (i0 >= sq.lq) return;
+  const int off = sq.lk - sq.lq;
+  auto kt_last = [&](int g) {
+    const int r0 = i0 + 32 * g;
+    return r0 < sq.lq ? (min(r0 + 32, sq.lq) - 1 + off) / C::kBN : -1;
+  };
+  const int nkt = max(max(kt_last(0), kt_last(1)), max(kt_last(2), kt_last(3))) + 1;
+  ker.ktm0 = kt_last(2 * ker.qpair);
+  ker.ktm1 = kt_last(2 * ker.qpair + 1);
+  ker.ktm_copy = kt_last(ker.wave >> 1);
+
+  ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
+  ker.kstride = a.kl.token_stride;
+  const int64_t row0 =
+      (sq.packed ? sq.qtok / 32 + s : (int64_t)s * ((p.seqlen_q + 31) / 32)) + i0 / 32;
+  ker.ds_col_stride = (int64_t)a.ds_rows * 4096;
+  ker.ds_col0 = (const char*)a.ds + ((int64_t)qh * a.ds_cols * a.ds_rows + row0) * 4096;
+  ker.trk.init(ker.lane, ker.dquart * 128 * 2);
+  ker.trs.init(ker.lane);
+  ker.kcp.init(ker.kstride, ker.wave, ker.lane);
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) ker.acc[g][b] = f32x16{};
+
+  const int g0 = 2 * ker.qpair;
+  if (nkt > 0) ker.issue(0, 0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int cur = kt & 1;
+    vm_wait<0>();
+    barrier_lds();  // tile kt landed; every wave is done with buffer cur ^ 1
+    if (kt + 1 < nkt) ker.issue(kt + 1, cur ^ 1);
+    const char G4_LDS* ktile = ker.smem + C::kLdsK + cur * C::kKTile;
+    const char G4_LDS* ds0 = ker.smem + C::kLdsDs + (cur * 4 + g0) * 4096;
+    const char G4_LDS* ds1 = ds0 + 4096;
+    const bool v0 = kt <= ker.ktm0, v1 = kt <= ker.ktm1;
+    ker.kstep<0>(ktile, ds0, ds1, v0, v1);
+    ker.kstep<1>(ktile, ds0, ds1, v0, v1);
+    ker.kstep<2>(ktile, ds0, ds1, v0, v1);
+    ker.kstep<3>(ktile, ds0, ds1, v0, v1);
+  }
+
+#pragma unroll
+  for (int g2 = 0; g2 < 2; ++g2) {
+    const int my_i = i0 + 32 * (g0 + g2) + l32;
+    if (my_i >= sq.lq) continue;
+    __bf16* row = a.dq + tok_off(sq, s, sq.qtok, my_i, a.dql) + (int64_t)qh * a.dql.head_stride;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = ker.dquart * 128 + b * 32 + 8 * r4 + 4 * ker.h32;
+        const f32x16& x = ker.acc[g2][b];
+        *(bf16x4*)(row + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
+                                     (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
+      }
+  }
+}
+
 }  // namespace
+
+static hipError_t launch_dq_ds(const BwdParams& a, hipStream_t stream) {
+  using C = DqDsCfg;
+  static bool done = false;
+  if (!done) {
+    hipError_t e = hipFuncSetAttribute((const void*)dq_ds_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+    if (e != hipSuccess) return e;
+    done = true;
+  }
+  BwdParams b = a;
+  b.ntiles = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
+  const int64_t nblocks = (int64_t)b.num_seqs * b.ntiles * a.p.num_q_heads;
+  if (nblocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(dq_ds_kernel, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream,
+                     b);
+  return hipGetLastError();
+}
 
 template <int D>
 hipError_t launch_dq_roles_d(const BwdParams& a, hipStream_t stream) {
@@ -1315,7 +1542,11 @@ hipError_t launch_dq_roles_d(const BwdParams& a, hipStream_t stream) {
 }
 
 hipError_t launch_bwd_dq(const BwdParams& a, hipStream_t stream) {
-  if (a.p.head_dim == 512) return launch_dq_roles_d<512>(a, stream);
+  if (a.p.head_dim == 512) {
+    // With the dK/dV kernel's dS tiles in the workspace, dQ is a plain product.
+    if (a.ds != nullptr) return launch_dq_ds(a, stream);
+    return launch_dq_roles_d<512>(a, stream);
+  }
   if (a.p.head_dim == 256) return launch_dq_roles_d<256>(a, stream);
   return hipErrorInvalidValue;
 }

@@ -42,12 +42,21 @@ struct BwdParams {
   const int* span_hi;
   int num_seqs;
   int ntiles;          // row tiles per sequence (set by the launchers)
+  // dS tiles of the head-dim 512 causal backward (null when not used): tile
+  // (query head h, key tile c, row r) at ((h * ds_cols + c) * ds_rows + r) * 4 KB,
+  // [64 keys][32 queries] bf16.  Row r of packed sequence s, query tile t is
+  // floor(cu_q[s] / 32) + s + t (fixed layouts: s * ceil(Sq / 32) + t).
+  __bf16* ds;
+  int ds_rows, ds_cols;
 };
 
 // Workspace layout helpers (bytes).
 size_t spans_bytes(const g4_problem& p);
 size_t delta_bytes(const g4_problem& p);
 size_t raise_flags_bytes(const g4_problem& p);
+// dS buffer of the head-dim 512 causal backward (0: the dQ stage recomputes S, dP).
+size_t ds_bytes(const g4_problem& p);
+void ds_geometry(const g4_problem& p, int* rows, int* cols);
 int64_t k_stream_tokens(const g4_problem& p);
 int64_t q_stream_tokens(const g4_problem& p);
 
