@@ -85,6 +85,7 @@ struct RolesKernel {
   int grp, kvh, qt_lo, nqt;
   int64_t tq;
   int64_t ds_row0;  // dS tile row of this sequence's first query tile
+  uint32_t ds_lane;  // byte offset of this lane's dS run inside a tile
   RowReader<C::kCPR> rrd;
   TrReader<C::kCPR> trd;
   TileCopier<C::kCPR, C::kBM, 4> qcp, docp;  // Q by the P waves, dO by the dS waves
@@ -283,19 +284,17 @@ struct RolesKernel {
           db[m][4 * q4 + e] = (__bf16)(pv[e] * (dp[r] - del4[e]));
         }
       }
-    if (a->ds != nullptr && dh == 0) {
-      // dS tile [64 keys][32 queries]: this lane's key row, four runs of four
-      // queries (rows 8 (r >> 2) + 4 h32 + (r & 3) of the accumulator layout).
-      char* row = (char*)a->ds +
-                  (((int64_t)qh * a->ds_cols + j0 / C::kBN) * a->ds_rows + ds_row0 + i0 / 32) *
-                      4096 +
-                  (kb * 32 + (lane & 31)) * 64;
-#pragma unroll
-      for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int q4 = 0; q4 < 2; ++q4)
-          *(bf16x4*)(row + (8 * (2 * m + q4) + 4 * h32) * 2) =
-              bf16x4{db[m][4 * q4], db[m][4 * q4 + 1], db[m][4 * q4 + 2], db[m][4 * q4 + 3]};
+    if (a->ds != nullptr) {
+      // dS tile [64 keys][32 queries]: this lane's key row holds four runs of
+      // four queries (rows 8 (r >> 2) + 4 h32 + (r & 3) of the accumulator
+      // layout); both waves of the pair hold all of them, wave dh stores the
+      // two runs of db[dh].
+      G4_GLOBAL char* tile =
+          (G4_GLOBAL char*)a->ds +
+          (((int64_t)qh * a->ds_cols + j0 / C::kBN) * a->ds_rows + ds_row0 + i0 / 32) * 4096;
+      const bf16x8 x = dh == 0 ? db[0] : db[1];
+      *(G4_GLOBAL bf16x4*)(tile + ds_lane) = bf16x4{x[0], x[1], x[2], x[3]};
+      *(G4_GLOBAL bf16x4*)(tile + ds_lane + 16) = bf16x4{x[4], x[5], x[6], x[7]};
     }
     __builtin_amdgcn_sched_barrier(0);
     acc_step<0, 0>(qt, db);
@@ -410,6 +409,7 @@ __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams 
   }
   const int nsteps = ker.nqt * ker.grp;
   ker.ds_row0 = sq.packed ? sq.qtok / 32 + ker.s : (int64_t)ker.s * ((p.seqlen_q + 31) / 32);
+  ker.ds_lane = (ker.kb * 32 + (ker.lane & 31)) * 64 + 32 * ker.dh + 8 * ker.h32;
   const int jc = min(ker.my_j, sq.lk - 1);
   ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + jc] : -1;
   ker.my_doc = ker.has_doc ? p.document_ids[sq.ktok + jc] : 0;
@@ -1347,10 +1347,8 @@ struct PlainTrReader {
   }
   template <int ROW0>
   __device__ __forceinline__ bf16x8 read(const char G4_LDS* tile) const {
-    bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-        (bf16x4 G4_LDS*)(tile + base[0] + ROW0 * 64));
-    bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-        (bf16x4 G4_LDS*)(tile + base[1] + ROW0 * 64));
+    bf16x4 lo = lds_read_tr<true>(tile + base[0] + ROW0 * 64);
+    bf16x4 hi = lds_read_tr<true>(tile + base[1] + ROW0 * 64);
     return cat4(lo, hi);
   }
 };

@@ -29,6 +29,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 #define G4_LDS __attribute__((address_space(3)))
+#define G4_GLOBAL __attribute__((address_space(1)))
 
 namespace g4 {
 
@@ -57,8 +58,25 @@ __device__ __forceinline__ bf16x8 lds_read16(const char G4_LDS* base, int off) {
   return *(const bf16x8 G4_LDS*)(base + off);
 }
 
-__device__ __forceinline__ bf16x4 lds_read_tr(const char G4_LDS* base, int off) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((bf16x4 G4_LDS*)(base + off));
+// Transposing 8-byte LDS reads (ds_read_b64_tr_b16).  Without alias-scope
+// metadata on the read the compiler's wait insertion ties it to every
+// outstanding buffer -> LDS copy and waits for them all (vmcnt 0) before it,
+// although the copies fill the other buffer.  The restrict-qualified
+// parameter of lds_read_tr_scoped gives the read that metadata once inlined,
+// so no such wait is inserted; every kernel here orders its copies and reads
+// itself (vm_wait before the barrier that publishes a copied buffer).
+__device__ __forceinline__ bf16x4 lds_read_tr_scoped(const char G4_LDS* __restrict__ p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((bf16x4 G4_LDS*)p);
+}
+__device__ __forceinline__ bf16x4 lds_read_tr_waited(const char G4_LDS* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((bf16x4 G4_LDS*)p);
+}
+template <bool SCOPED>
+__device__ __forceinline__ bf16x4 lds_read_tr(const char G4_LDS* p) {
+  if constexpr (SCOPED)
+    return lds_read_tr_scoped(p);
+  else
+    return lds_read_tr_waited(p);
 }
 
 __device__ __forceinline__ bf16x8 cat4(bf16x4 a, bf16x4 b) {
@@ -89,6 +107,11 @@ __device__ __forceinline__ float wave_xor32(float x) {
 __device__ __forceinline__ void barrier_lds() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+
+// Wait for every vector-memory operation of this wave, through the compiler's
+// own wait instruction (vmcnt 0, expcnt and lgkmcnt at their maxima), so that
+// its wait insertion knows that nothing is outstanding afterwards.
+__device__ __forceinline__ void vm_wait_seen0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Wait until at most N vector-memory operations of this wave are outstanding.
 template <int N>
@@ -143,8 +166,8 @@ struct RowReader {
 // from a row-major swizzled tile: lane l gets column 16*((l>>4)&1) + (l&15)
 // and rows {4h + e, 8 + 4h + e}.  Chunk 4 bq + lb sits in slot
 // 4 (bq ^ (sw >> 2)) + (lb ^ (sw & 3)), so each of the two row groups needs
-// one per-lane base with 64 bq XORed into bits 6-7.
-template <int CPR>
+// one per-lane base with 64 bq XORed into bits 6-7.  SCOPED: see lds_read_tr.
+template <int CPR, bool SCOPED = true>
 struct TrReader {
   int base[2];
   __device__ __forceinline__ void init(int lane, int b = 0) {
@@ -163,10 +186,8 @@ struct TrReader {
   __device__ __forceinline__ bf16x8 read(const char G4_LDS* tile) const {
     static_assert(ROW0 % 16 == 0 && CBASE % 16 == 0, "alignment");
     constexpr int imm = (ROW0 * CPR + CBASE + 16 * (B >> 2)) * 16;
-    bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-        (bf16x4 G4_LDS*)(tile + (base[0] ^ (64 * (B & 3))) + imm));
-    bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-        (bf16x4 G4_LDS*)(tile + (base[1] ^ (64 * (B & 3))) + imm));
+    bf16x4 lo = lds_read_tr<SCOPED>(tile + (base[0] ^ (64 * (B & 3))) + imm);
+    bf16x4 hi = lds_read_tr<SCOPED>(tile + (base[1] ^ (64 * (B & 3))) + imm);
     return cat4(lo, hi);
   }
 };

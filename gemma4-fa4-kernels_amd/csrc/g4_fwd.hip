@@ -69,7 +69,9 @@ struct FwdKernel {
   const __bf16* vbase;
   int64_t kstride, vstride;
   RowReader<C::kCPR> krd;
-  TrReader<C::kCPR> vrd;
+  // Head dim 512 keeps the compiler's wait before the P.V reads: with it the
+  // 8192-token causal forward measured 2.81 ms, without it 2.91 ms.
+  TrReader<C::kCPR, (D != 512)> vrd;
   TileCopier<C::kCPR, BN, C::kNW, (OCC > 1)> kcp, vcp;
   bf16x8 qf[kNC];
   f32x16 o_acc[kNB];
@@ -490,7 +492,7 @@ struct FwdWide {
   const __bf16* vbase;
   int64_t kstride, vstride;
   RowReader<C::kCPR> krd;
-  TrReader<C::kCPR> vrd;
+  TrReader<C::kCPR, false> vrd;  // as FwdKernel's at head dim 512
   TileCopier<C::kCPR, BN, C::kNW> kcp, vcp;
   bf16x8 qf[kNC];
   f32x16 o_acc[kNB];
