@@ -108,11 +108,6 @@ __device__ __forceinline__ void barrier_lds() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Wait for every vector-memory operation of this wave, through the compiler's
-// own wait instruction (vmcnt 0, expcnt and lgkmcnt at their maxima), so that
-// its wait insertion knows that nothing is outstanding afterwards.
-__device__ __forceinline__ void vm_wait_seen0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
 // Wait until at most N vector-memory operations of this wave are outstanding.
 template <int N>
 __device__ __forceinline__ void vm_wait() {
