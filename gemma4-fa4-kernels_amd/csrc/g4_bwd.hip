@@ -1,4 +1,4 @@
-// Backward pre-pass: delta[h, t] = rowsum(O * dO) - dLSE (fp32), one wave per row.
+// Backward pre-pass: delta[h, t] = rowsum(O * dO) - dLSE (fp32).
 #include "g4_kernels.h"
 
 namespace g4 {
@@ -20,32 +20,50 @@ __device__ inline void seq_of_qtoken(const g4_problem& p, int64_t t, int& s, int
   i = (int)(t - p.cu_seqlens_q[lo]);
 }
 
+// One wave per (query token, group of kHG query heads): every lane loads its
+// 16-byte chunks of the group's O and dO rows before any reduction, so a wave
+// keeps 2 * kHG * D * 2 bytes in flight; 64 / CPR heads share each load
+// instruction (CPR = D / 8 chunks per row) and each head's dot product is
+// reduced over its CPR lanes.
 template <int D>
 __global__ void __launch_bounds__(256) delta_kernel(BwdParams a, int64_t tq) {
+  constexpr int CPR = D / 8;          // 16-byte chunks per head row
+  constexpr int HPI = 64 / CPR;       // heads per load instruction
+  constexpr int kHG = 8;              // heads per wave item
+  constexpr int NI = kHG / HPI;       // load instructions per operand
   const int lane = threadIdx.x & 63;
-  const int64_t rows = tq * a.p.num_q_heads;
-  for (int64_t r = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / 64; r < rows;
+  const int hq = a.p.num_q_heads;
+  const int groups = (hq + kHG - 1) / kHG;
+  const int64_t items = tq * groups;
+  const int c = lane % CPR, hl = lane / CPR;
+  for (int64_t r = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / 64; r < items;
        r += (int64_t)gridDim.x * blockDim.x / 64) {
-    const int64_t t = r / a.p.num_q_heads;
-    const int h = (int)(r % a.p.num_q_heads);
+    const int64_t t = r / groups;
+    const int h0 = (int)(r % groups) * kHG;
     int s, i;
     seq_of_qtoken(a.p, t, s, i);
     const Seq sq = resolve_seq(a.p, s);
-    const __bf16* orow = a.o + tok_off(sq, s, sq.qtok, i, a.ol) + (int64_t)h * a.ol.head_stride;
-    const __bf16* grow =
-        a.dout + tok_off(sq, s, sq.qtok, i, a.dol) + (int64_t)h * a.dol.head_stride;
-    float acc = 0.f;
+    const __bf16* obase = a.o + tok_off(sq, s, sq.qtok, i, a.ol) + c * 8;
+    const __bf16* gbase = a.dout + tok_off(sq, s, sq.qtok, i, a.dol) + c * 8;
+    bf16x8 x[NI], y[NI];
 #pragma unroll
-    for (int c = lane * 8; c < D; c += 512) {
-      bf16x8 x = ld_global16(orow + c), y = ld_global16(grow + c);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (float)x[e] * (float)y[e];
+    for (int u = 0; u < NI; ++u) {
+      const int h = min(h0 + u * HPI + hl, hq - 1);
+      x[u] = ld_global16(obase + (int64_t)h * a.ol.head_stride);
+      y[u] = ld_global16(gbase + (int64_t)h * a.dol.head_stride);
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (lane == 0) {
-      float dl = a.dlse ? a.dlse[lse_off(a.p, sq, s, h, i)] : 0.f;
-      a.delta[(int64_t)h * tq + t] = acc - dl;
+    for (int u = 0; u < NI; ++u) {
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)x[u][e] * (float)y[u][e];
+#pragma unroll
+      for (int o = CPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+      const int h = h0 + u * HPI + hl;
+      if (c == 0 && h < hq) {
+        const float dl = a.dlse ? a.dlse[lse_off(a.p, sq, s, h, i)] : 0.f;
+        a.delta[(int64_t)h * tq + t] = acc - dl;
+      }
     }
   }
 }
@@ -54,9 +72,9 @@ __global__ void __launch_bounds__(256) delta_kernel(BwdParams a, int64_t tq) {
 
 hipError_t launch_bwd_delta(const BwdParams& a, hipStream_t stream) {
   const int64_t tq = q_stream_tokens(a.p);
-  const int64_t rows = tq * a.p.num_q_heads;
-  int64_t blocks = (rows + 3) / 4;
-  if (blocks > 65536) blocks = 65536;
+  const int64_t items = tq * ((a.p.num_q_heads + 7) / 8);  // waves of work (kHG = 8)
+  int64_t blocks = (items + 3) / 4;
+  if (blocks > 8192) blocks = 8192;
   if (a.p.head_dim == 256)
     delta_kernel<256><<<(unsigned)blocks, 256, 0, stream>>>(a, tq);
   else
