@@ -341,11 +341,12 @@ struct RolesKernel {
   }
 };
 
+// One key tile kt of sequence s and KV head kvh.
 template <bool META>
-__global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams a) {
+__device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_raw, int kvh,
+                                                int s, int kt) {
   using K = RolesKernel<META>;
   using C = RolesCfg;
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   K ker;
   ker.smem = (char G4_LDS*)smem_raw;
   ker.a = &a;
@@ -359,14 +360,9 @@ __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams 
   ker.dh = ker.slot & 1;
   ker.h32 = ker.lane >> 5;
 
-  // ---- work item: (sequence, key tile, KV head) ------------------------------
   ker.grp = p.num_q_heads / p.num_kv_heads;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int per_kvh = a.num_seqs * a.ntiles;
-  ker.kvh = L / per_kvh;
-  const int rank = L % per_kvh;
-  ker.s = rank / a.ntiles;
-  const int kt = zigzag(rank % a.ntiles, a.ntiles);
+  ker.kvh = kvh;
+  ker.s = s;
   ker.sq = resolve_seq(p, ker.s);
   const Seq& sq = ker.sq;
   ker.j0 = kt * C::kBN;
@@ -429,6 +425,38 @@ __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams 
     ker.template run<true>(nsteps);
   else
     ker.template run<false>(nsteps);
+}
+
+// Work item: (KV head, sequence, pair r) = key tiles r and nt - 1 - r of the
+// sequence (nt = its key tiles).  Under the causal mask a key tile's query
+// count falls linearly with its index, so every pair carries about the same
+// number of steps; with one workgroup per CU (the LDS holds one) this keeps
+// every CU equally busy, which the hardware's dispatch of one tile per
+// workgroup did not (per-CU busy time ranged from 8% to 100% of the launch on
+// an 8192-token causal sequence).
+template <bool META>
+__global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams a) {
+  using C = RolesCfg;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  const int npairs = (a.ntiles + 1) / 2;
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_kvh = a.num_seqs * npairs;
+  const int kvh = L / per_kvh;
+  const int rank = L % per_kvh;
+  const int s = rank / npairs;
+  const int r = rank % npairs;
+  const Seq sq = resolve_seq(a.p, s);
+  const int nt = (sq.lk + C::kBN - 1) / C::kBN;
+  if (r >= (nt + 1) / 2) return;
+#pragma nounroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int kt = pass == 0 ? r : nt - 1 - r;
+    if (pass == 1) {
+      if (kt == r) break;
+      barrier_lds();  // every wave is done with the first tile's LDS
+    }
+    dkdv_roles_tile<META>(a, smem_raw, kvh, s, kt);
+  }
 }
 
 // ===========================================================================
@@ -1568,7 +1596,9 @@ hipError_t launch_dkdv_roles_d(const BwdParams& a, hipStream_t stream) {
   }
   BwdParams b = a;
   b.ntiles = (a.p.seqlen_k + C::kBN - 1) / C::kBN;
-  const int64_t nblocks = (int64_t)b.num_seqs * b.ntiles * a.p.num_kv_heads;
+  // Head dim 512: one workgroup per pair of key tiles (see dkdv_roles_kernel).
+  const int64_t per_seq = D == 512 ? (b.ntiles + 1) / 2 : b.ntiles;
+  const int64_t nblocks = (int64_t)b.num_seqs * per_seq * a.p.num_kv_heads;
   if (nblocks <= 0) return hipSuccess;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();
