@@ -87,7 +87,7 @@ int check_ws(const g4_problem* p, int phase, void* ws, size_t bytes) {
     if (_rc != G4_OK) return _rc; \
   } while (0)
 
-// Workspace: [spans][raise flags][delta]
+// Workspace: [spans][raise flags] (forward); backward adds [delta][dS][queue counters]
 int* raise_flags_ptr(const g4_problem& p, void* ws) {
   return g4::raise_flags_bytes(p) ? (int*)((char*)ws + align256(g4::spans_bytes(p))) : nullptr;
 }
@@ -98,6 +98,10 @@ __bf16* ds_ptr(const g4_problem& p, void* ws) {
   if (!g4::ds_bytes(p)) return nullptr;
   return (__bf16*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) +
                    g4::delta_bytes(p));
+}
+unsigned* sched_ptr(const g4_problem& p, void* ws) {
+  return (unsigned*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) +
+                     g4::delta_bytes(p) + g4::ds_bytes(p));
 }
 
 }  // namespace
@@ -142,7 +146,7 @@ const char* g4_last_error(void) { return g_last_error.c_str(); }
 size_t g4_workspace_bytes(const g4_problem* p, int phase) {
   if (check_problem(p) != G4_OK) return 0;
   size_t b = align256(g4::spans_bytes(*p)) + g4::raise_flags_bytes(*p);
-  if (phase == 1) b += g4::delta_bytes(*p) + g4::ds_bytes(*p);
+  if (phase == 1) b += g4::delta_bytes(*p) + g4::ds_bytes(*p) + g4::kSchedBytes;
   return b;
 }
 
@@ -193,6 +197,7 @@ static int fill_bwd(g4::BwdParams& a, const g4_problem* p, const void* q, g4_lay
   a.delta = delta_ptr(*p, ws);
   a.ds = ds_ptr(*p, ws);
   g4::ds_geometry(*p, &a.ds_rows, &a.ds_cols);
+  a.sched = sched_ptr(*p, ws);
   g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);
   return G4_OK;
 }
@@ -211,6 +216,7 @@ int g4_attn_bwd_delta(const g4_problem* p, const void* o, g4_layout ol, const vo
   a.dol = dol;
   a.dlse = dlse;
   a.num_seqs = p->num_seqs;
+  a.sched = sched_ptr(*p, ws);
   a.delta = delta_ptr(*p, ws);
   hipStream_t st = (hipStream_t)stream;
   if (g4::spans_bytes(*p)) {

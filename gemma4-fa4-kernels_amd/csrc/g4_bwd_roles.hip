@@ -39,6 +39,8 @@
 // P in fp32 and the fixed-order dP sum keep the numerics of a single-wave
 // formulation: dS = bf16(P (dP - delta)), dV from bf16(P).  No atomics; every
 // output element is written by one wave.
+#include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "g4_kernels.h"
@@ -46,6 +48,17 @@
 namespace g4 {
 
 namespace {
+
+// Thread index as seen by one work item.  In a queue kernel (QUEUE) it passes
+// through an empty asm, so the per-lane offsets derived from it are formed in
+// each item rather than hoisted out of the ticket loop into registers held
+// across all items (which then spill inside the step loops).
+template <bool QUEUE>
+__device__ __forceinline__ int item_thread_id() {
+  int t = threadIdx.x;
+  if constexpr (QUEUE) asm volatile("" : "+v"(t));
+  return t;
+}
 
 struct RolesCfg {
   static constexpr int D = 512;
@@ -342,7 +355,7 @@ struct RolesKernel {
 };
 
 // One key tile kt of sequence s and KV head kvh.
-template <bool META>
+template <bool META, bool QUEUE>
 __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_raw, int kvh,
                                                 int s, int kt) {
   using K = RolesKernel<META>;
@@ -351,7 +364,7 @@ __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_r
   ker.smem = (char G4_LDS*)smem_raw;
   ker.a = &a;
   const g4_problem& p = a.p;
-  const int tid = threadIdx.x;
+  const int tid = item_thread_id<QUEUE>();
   ker.lane = tid & 63;
   ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool pwave = ker.wave < 4;
@@ -427,24 +440,21 @@ __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_r
     ker.template run<false>(nsteps);
 }
 
-// Work item: (KV head, sequence, pair r) = key tiles r and nt - 1 - r of the
-// sequence (nt = its key tiles).  Under the causal mask a key tile's query
-// count falls linearly with its index, so every pair carries about the same
-// number of steps; with one workgroup per CU (the LDS holds one) this keeps
-// every CU equally busy, which the hardware's dispatch of one tile per
-// workgroup did not (per-CU busy time ranged from 8% to 100% of the launch on
-// an 8192-token causal sequence).
-template <bool META>
-__global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams a) {
+// Work item L: (KV head, pair r, sequence) = key tiles r and nt - 1 - r of
+// the sequence (nt = its key tiles), the largest r (present only in the
+// longest sequences) first within a KV head.  Under the causal mask a key
+// tile's query count falls linearly with its index, so a pair carries about
+// the same number of steps whatever r is.  KV head slowest keeps the
+// workgroups of one XCD on one head group's Q and dO.
+template <bool META, bool QUEUE>
+__device__ __forceinline__ void dkdv_roles_pair(const BwdParams& a, char* smem_raw, int L) {
   using C = RolesCfg;
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   const int npairs = (a.ntiles + 1) / 2;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int per_kvh = a.num_seqs * npairs;
+  const int per_kvh = npairs * a.num_seqs;
   const int kvh = L / per_kvh;
-  const int rank = L % per_kvh;
-  const int s = rank / npairs;
-  const int r = rank % npairs;
+  const int rem = L % per_kvh;
+  const int r = npairs - 1 - rem / a.num_seqs;
+  const int s = rem % a.num_seqs;
   const Seq sq = resolve_seq(a.p, s);
   const int nt = (sq.lk + C::kBN - 1) / C::kBN;
   if (r >= (nt + 1) / 2) return;
@@ -455,7 +465,26 @@ __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams 
       if (kt == r) break;
       barrier_lds();  // every wave is done with the first tile's LDS
     }
-    dkdv_roles_tile<META>(a, smem_raw, kvh, s, kt);
+    dkdv_roles_tile<META, QUEUE>(a, smem_raw, kvh, s, kt);
+  }
+}
+
+// Persistent: a few workgroups per CU take pair tickets from the dK/dV work
+// queue.  (With one workgroup per key tile, per-CU busy time on an 8192-token
+// causal sequence ranged from 8% to 100% of the launch.)
+template <bool META, bool QUEUE>
+__global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams a) {
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  if constexpr (QUEUE) {
+    const int n = (a.ntiles + 1) / 2 * a.num_seqs * a.p.num_kv_heads;
+    WorkQueue wq{a.sched, n, 0};
+    for (;;) {
+      const int t = wq.next((int G4_LDS*)smem_raw);
+      if (t >= n) break;
+      dkdv_roles_pair<META, true>(a, smem_raw, t);
+    }
+  } else {
+    dkdv_roles_pair<META, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
   }
 }
 
@@ -689,16 +718,16 @@ struct Roles256Kernel {
   }
 };
 
-template <bool META>
-__global__ void __launch_bounds__(Roles256Cfg::kNT, 1) dkdv_roles256_kernel(BwdParams a) {
+// Work item L: (KV head, sequence, key tile).
+template <bool META, bool QUEUE>
+__device__ __forceinline__ void dkdv_roles256_item(const BwdParams& a, char* smem_raw, int L) {
   using K = Roles256Kernel<META>;
   using C = Roles256Cfg;
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   K ker;
   ker.smem = (char G4_LDS*)smem_raw;
   ker.a = &a;
   const g4_problem& p = a.p;
-  const int tid = threadIdx.x;
+  const int tid = item_thread_id<QUEUE>();
   ker.lane = tid & 63;
   ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool pwave = ker.wave < 4;
@@ -706,7 +735,6 @@ __global__ void __launch_bounds__(Roles256Cfg::kNT, 1) dkdv_roles256_kernel(BwdP
   ker.h32 = ker.lane >> 5;
 
   ker.grp = p.num_q_heads / p.num_kv_heads;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int per_kvh = a.num_seqs * a.ntiles;
   ker.kvh = L / per_kvh;
   const int rank = L % per_kvh;
@@ -771,6 +799,24 @@ __global__ void __launch_bounds__(Roles256Cfg::kNT, 1) dkdv_roles256_kernel(BwdP
     ker.template run<true>(nsteps);
   else
     ker.template run<false>(nsteps);
+}
+
+// Persistent: a few workgroups per CU take (KV head, sequence, key tile)
+// tickets from the dK/dV work queue.
+template <bool META, bool QUEUE>
+__global__ void __launch_bounds__(Roles256Cfg::kNT, 1) dkdv_roles256_kernel(BwdParams a) {
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  if constexpr (QUEUE) {
+    const int n = a.num_seqs * a.ntiles * a.p.num_kv_heads;
+    WorkQueue wq{a.sched, n, 0};
+    for (;;) {
+      const int t = wq.next((int G4_LDS*)smem_raw);
+      if (t >= n) break;
+      dkdv_roles256_item<META, true>(a, smem_raw, t);
+    }
+  } else {
+    dkdv_roles256_item<META, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
+  }
 }
 
 // ===========================================================================
@@ -1220,16 +1266,16 @@ struct DqRoles256Kernel {
   }
 };
 
-template <bool META>
-__global__ void __launch_bounds__(DqRoles256Cfg::kNT, 1) dq_roles256_kernel(BwdParams a) {
+// Work item L: (KV head, sequence, query tile, head of the group).
+template <bool META, bool QUEUE>
+__device__ __forceinline__ void dq_roles256_item(const BwdParams& a, char* smem_raw, int L) {
   using K = DqRoles256Kernel<META>;
   using C = DqRoles256Cfg;
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   K ker;
   ker.smem = (char G4_LDS*)smem_raw;
   ker.a = &a;
   const g4_problem& p = a.p;
-  const int tid = threadIdx.x;
+  const int tid = item_thread_id<QUEUE>();
   ker.lane = tid & 63;
   ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   ker.role = ker.wave >> 2;
@@ -1238,7 +1284,6 @@ __global__ void __launch_bounds__(DqRoles256Cfg::kNT, 1) dq_roles256_kernel(BwdP
   const int l32 = ker.lane & 31;
 
   const int grp = p.num_q_heads / p.num_kv_heads;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int per_kvh = a.num_seqs * a.ntiles * grp;
   const int kvh = L / per_kvh;
   const int rem = L % per_kvh;
@@ -1330,6 +1375,24 @@ __global__ void __launch_bounds__(DqRoles256Cfg::kNT, 1) dq_roles256_kernel(BwdP
         *(bf16x4*)(row + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
                                      (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
       }
+  }
+}
+
+// Persistent: a few workgroups per CU take query-tile tickets from the dQ
+// work queue.
+template <bool META, bool QUEUE>
+__global__ void __launch_bounds__(DqRoles256Cfg::kNT, 1) dq_roles256_kernel(BwdParams a) {
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  if constexpr (QUEUE) {
+    const int n = a.num_seqs * a.ntiles * a.p.num_q_heads;
+    WorkQueue wq{a.sched + 2, n, 0};
+    for (;;) {
+      const int t = wq.next((int G4_LDS*)smem_raw);
+      if (t >= n) break;
+      dq_roles256_item<META, true>(a, smem_raw, t);
+    }
+  } else {
+    dq_roles256_item<META, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
   }
 }
 
@@ -1436,14 +1499,16 @@ struct DqDsKernel {
   }
 };
 
-__global__ void __launch_bounds__(DqDsCfg::kNT, 1) dq_ds_kernel(BwdParams a) {
+// Work item L: query tile (last, i.e. heaviest under the causal mask, first),
+// then sequence, then query head.
+template <bool QUEUE>
+__device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, int L) {
   using C = DqDsCfg;
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   DqDsKernel ker;
   ker.smem = (char G4_LDS*)smem_raw;
   ker.a = &a;
   const g4_problem& p = a.p;
-  const int tid = threadIdx.x;
+  const int tid = item_thread_id<QUEUE>();
   ker.lane = tid & 63;
   ker.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   ker.h32 = ker.lane >> 5;
@@ -1452,14 +1517,12 @@ __global__ void __launch_bounds__(DqDsCfg::kNT, 1) dq_ds_kernel(BwdParams a) {
   const int l32 = ker.lane & 31;
 
   const int grp = p.num_q_heads / p.num_kv_heads;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int per_kvh = a.num_seqs * a.ntiles * grp;
-  const int kvh = L / per_kvh;
-  const int rem = L % per_kvh;
-  const int rank = rem / grp;
-  const int qh = kvh * grp + rem % grp;
-  const int s = rank / a.ntiles;
-  const int qt = zigzag(rank % a.ntiles, a.ntiles);
+  const int per_qt = a.num_seqs * p.num_q_heads;
+  const int qt = a.ntiles - 1 - L / per_qt;
+  const int rem = L % per_qt;
+  const int s = rem / p.num_q_heads;
+  const int qh = rem % p.num_q_heads;
+  const int kvh = qh / grp;
   ker.sq = resolve_seq(p, s);
   const Seq& sq = ker.sq;
   const int i0 = qt * C::kBM;
@@ -1522,23 +1585,72 @@ __global__ void __launch_bounds__(DqDsCfg::kNT, 1) dq_ds_kernel(BwdParams a) {
   }
 }
 
+// Persistent: a few workgroups per CU take query-tile tickets from the dQ
+// work queue, the heaviest tiles first.
+template <bool QUEUE>
+__global__ void __launch_bounds__(DqDsCfg::kNT, 1) dq_ds_kernel(BwdParams a) {
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  if constexpr (QUEUE) {
+    const int n = a.num_seqs * a.ntiles * a.p.num_q_heads;
+    WorkQueue wq{a.sched + 2, n, 0};
+    for (;;) {
+      const int t = wq.next((int G4_LDS*)smem_raw);
+      if (t >= n) break;
+      dq_ds_item<true>(a, smem_raw, t);
+    }
+  } else {
+    dq_ds_item<false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
+  }
+}
+
 }  // namespace
+
+// Launch shape of a tile kernel: with more than kQueueMin items per resident
+// workgroup (CUs x workgroups per CU from the occupancy query of the queue
+// variant) the queue variant on as many workgroups as are resident at once;
+// otherwise the plain variant, one workgroup per item (with few items per CU
+// the queue's draws and the lost XCD locality of later tickets cost more than
+// the balance gains: measured on configs 1 and 3).
+struct PersistentGrid {
+  static constexpr int kQueueMin = 4;
+  std::atomic<int> resident{0};
+  // Workgroups of the launch; *queue says which variant.
+  int64_t size(const void* queue_kern, int threads, int lds, int64_t items, bool* queue) {
+    int n = resident.load(std::memory_order_relaxed);
+    if (n == 0) {
+      int dev = 0, cus = 0, per_cu = 0;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, queue_kern, threads, lds) !=
+              hipSuccess)
+        return 0;
+      n = cus * std::max(per_cu, 1);
+      resident.store(n, std::memory_order_relaxed);
+    }
+    *queue = items > (int64_t)kQueueMin * n;
+    return *queue ? n : items;
+  }
+};
 
 static hipError_t launch_dq_ds(const BwdParams& a, hipStream_t stream) {
   using C = DqDsCfg;
-  static bool done = false;
-  if (!done) {
-    hipError_t e = hipFuncSetAttribute((const void*)dq_ds_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
-    if (e != hipSuccess) return e;
-    done = true;
-  }
+  static bool done[2] = {false, false};
   BwdParams b = a;
   b.ntiles = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
-  const int64_t nblocks = (int64_t)b.num_seqs * b.ntiles * a.p.num_q_heads;
-  if (nblocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(dq_ds_kernel, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream,
-                     b);
+  const int64_t items = (int64_t)b.num_seqs * b.ntiles * a.p.num_q_heads;
+  if (items <= 0) return hipSuccess;
+  static PersistentGrid grid;
+  bool queue = false;
+  const int64_t nblocks = grid.size((const void*)dq_ds_kernel<true>, C::kNT, C::kLdsBytes, items, &queue);
+  if (nblocks <= 0) return hipErrorInvalidValue;
+  void (*kern)(BwdParams) = queue ? dq_ds_kernel<true> : dq_ds_kernel<false>;
+  if (!done[queue]) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
+    if (e != hipSuccess) return e;
+    done[queue] = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();
 }
 
@@ -1547,22 +1659,32 @@ hipError_t launch_dq_roles_d(const BwdParams& a, hipStream_t stream) {
   using C = std::conditional_t<D == 512, DqRolesCfg, DqRoles256Cfg>;
   const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
                     a.p.document_ids != nullptr;
+  BwdParams b = a;
+  b.ntiles = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
+  const int64_t items = (int64_t)b.num_seqs * b.ntiles * a.p.num_q_heads;
+  if (items <= 0) return hipSuccess;
+  int64_t nblocks = items;  // head dim 512: one workgroup per query tile
+  bool queue = false;
   void (*kern)(BwdParams);
-  if constexpr (D == 512)
+  if constexpr (D == 512) {
     kern = meta ? dq_roles_kernel<true> : dq_roles_kernel<false>;
-  else
-    kern = meta ? dq_roles256_kernel<true> : dq_roles256_kernel<false>;
-  static bool done[2] = {false, false};
-  if (!done[meta]) {
+  } else {
+    static PersistentGrid grid;
+    nblocks = grid.size((const void*)(meta ? dq_roles256_kernel<true, true>
+                                           : dq_roles256_kernel<false, true>),
+                        C::kNT, C::kLdsBytes, items, &queue);
+    if (nblocks <= 0) return hipErrorInvalidValue;
+    kern = meta ? (queue ? dq_roles256_kernel<true, true> : dq_roles256_kernel<true, false>)
+                : (queue ? dq_roles256_kernel<false, true> : dq_roles256_kernel<false, false>);
+  }
+  static bool done[4] = {false, false, false, false};
+  const int v = 2 * meta + queue;
+  if (!done[v]) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
     if (e != hipSuccess) return e;
-    done[meta] = true;
+    done[v] = true;
   }
-  BwdParams b = a;
-  b.ntiles = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
-  const int64_t nblocks = (int64_t)b.num_seqs * b.ntiles * a.p.num_q_heads;
-  if (nblocks <= 0) return hipSuccess;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();
 }
@@ -1582,24 +1704,38 @@ hipError_t launch_dkdv_roles_d(const BwdParams& a, hipStream_t stream) {
   using C = std::conditional_t<D == 512, RolesCfg, Roles256Cfg>;
   const bool meta = (a.p.vision_ids != nullptr && a.p.bidirectional_vision) ||
                     a.p.document_ids != nullptr;
-  void (*kern)(BwdParams);
-  if constexpr (D == 512)
-    kern = meta ? dkdv_roles_kernel<true> : dkdv_roles_kernel<false>;
-  else
-    kern = meta ? dkdv_roles256_kernel<true> : dkdv_roles256_kernel<false>;
-  static bool done[2] = {false, false};
-  if (!done[meta]) {
+  BwdParams b = a;
+  b.ntiles = (a.p.seqlen_k + C::kBN - 1) / C::kBN;
+  // Head dim 512: one item per pair of key tiles (see dkdv_roles_pair).
+  const int64_t per_seq = D == 512 ? (b.ntiles + 1) / 2 : b.ntiles;
+  const int64_t items = (int64_t)b.num_seqs * per_seq * a.p.num_kv_heads;
+  if (items <= 0) return hipSuccess;
+  void (*kq[2])(BwdParams);  // [meta] queue variants
+  void (*ks[2])(BwdParams);  // [meta] one workgroup per item
+  if constexpr (D == 512) {
+    kq[0] = dkdv_roles_kernel<false, true>;
+    kq[1] = dkdv_roles_kernel<true, true>;
+    ks[0] = dkdv_roles_kernel<false, false>;
+    ks[1] = dkdv_roles_kernel<true, false>;
+  } else {
+    kq[0] = dkdv_roles256_kernel<false, true>;
+    kq[1] = dkdv_roles256_kernel<true, true>;
+    ks[0] = dkdv_roles256_kernel<false, false>;
+    ks[1] = dkdv_roles256_kernel<true, false>;
+  }
+  static PersistentGrid grid;
+  bool queue = false;
+  const int64_t nblocks = grid.size((const void*)kq[meta], C::kNT, C::kLdsBytes, items, &queue);
+  if (nblocks <= 0) return hipErrorInvalidValue;
+  void (*kern)(BwdParams) = queue ? kq[meta] : ks[meta];
+  static bool done[4] = {false, false, false, false};
+  const int v = 2 * meta + queue;
+  if (!done[v]) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
     if (e != hipSuccess) return e;
-    done[meta] = true;
+    done[v] = true;
   }
-  BwdParams b = a;
-  b.ntiles = (a.p.seqlen_k + C::kBN - 1) / C::kBN;
-  // Head dim 512: one workgroup per pair of key tiles (see dkdv_roles_kernel).
-  const int64_t per_seq = D == 512 ? (b.ntiles + 1) / 2 : b.ntiles;
-  const int64_t nblocks = (int64_t)b.num_seqs * per_seq * a.p.num_kv_heads;
-  if (nblocks <= 0) return hipSuccess;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();
 }

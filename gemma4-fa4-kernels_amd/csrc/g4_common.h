@@ -115,6 +115,8 @@ __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+
+
 // Async 16-byte buffer -> LDS copy from a wave-uniform base with a 32-bit
 // per-lane byte offset (raw buffer, no stride, 2 GiB range): lane l writes LDS
 // bytes [lds_wave_base + 16 l, +16).  The offset stays a single 32-bit VGPR.
@@ -413,5 +415,35 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
 __device__ __forceinline__ int zigzag(int r, int n) {
   return (r & 1) ? (r >> 1) : (n - 1 - (r >> 1));
 }
+
+// Work queue of a persistent launch (at most as many workgroups as are
+// resident at once, each taking tiles until they run out), so every CU stays
+// busy to the end however unevenly the tiles' costs or the hardware's
+// workgroup placement fall.  Workgroup b first takes item xcd_remap(b) (no
+// atomic; each XCD starts on a contiguous range), then tickets
+// gridDim.x + atomicAdd(counter, 1).  The n draws of a launch return the old
+// values 0 .. n - 1; the workgroup that draws n - 1 is the last to draw and
+// zeroes the counter for the next launch on the same workspace (the first
+// launch relies on it being zero).  A later ticket passes through an LDS slot
+// that lies in the tile area, so no copy may be in flight into it.
+struct WorkQueue {
+  unsigned* counter;
+  int n;      // work items
+  int taken;  // items this workgroup has started
+  __device__ __forceinline__ int next(int G4_LDS* slot) {
+    if (taken++ == 0) return xcd_remap(blockIdx.x, gridDim.x);
+    vm_wait<0>();
+    barrier_lds();  // every wave is done with the previous item's LDS
+    if (threadIdx.x == 0) {
+      const unsigned old = atomicAdd(counter, 1u);
+      if (old == (unsigned)n - 1u) atomicExch(counter, 0u);
+      *slot = (int)(gridDim.x + old);
+    }
+    barrier_lds();
+    const int t = __builtin_amdgcn_readfirstlane(*slot);
+    barrier_lds();  // every wave has read the slot before the next item's copies
+    return t;
+  }
+};
 
 }  // namespace g4

@@ -48,12 +48,16 @@ struct BwdParams {
   // floor(cu_q[s] / 32) + s + t (fixed layouts: s * ceil(Sq / 32) + t).
   __bf16* ds;
   int ds_rows, ds_cols;
+  // Work-queue ticket counters of the persistent tile kernels: [0] dK/dV,
+  // [2] dQ; zeroed by the delta pass, and by each launch's last draw.
+  unsigned* sched;
 };
 
 // Workspace layout helpers (bytes).
 size_t spans_bytes(const g4_problem& p);
 size_t delta_bytes(const g4_problem& p);
 size_t raise_flags_bytes(const g4_problem& p);
+constexpr size_t kSchedBytes = 256;  // work-queue counters (backward workspace tail)
 // dS buffer of the head-dim 512 causal backward (0: the dQ stage recomputes S, dP).
 size_t ds_bytes(const g4_problem& p);
 void ds_geometry(const g4_problem& p, int* rows, int* cols);
