@@ -49,16 +49,6 @@ namespace g4 {
 
 namespace {
 
-// Thread index as seen by one work item.  In a queue kernel (QUEUE) it passes
-// through an empty asm, so the per-lane offsets derived from it are formed in
-// each item rather than hoisted out of the ticket loop into registers held
-// across all items (which then spill inside the step loops).
-template <bool QUEUE>
-__device__ __forceinline__ int item_thread_id() {
-  int t = threadIdx.x;
-  if constexpr (QUEUE) asm volatile("" : "+v"(t));
-  return t;
-}
 
 struct RolesCfg {
   static constexpr int D = 512;
@@ -1605,32 +1595,6 @@ __global__ void __launch_bounds__(DqDsCfg::kNT, 1) dq_ds_kernel(BwdParams a) {
 
 }  // namespace
 
-// Launch shape of a tile kernel: with more than kQueueMin items per resident
-// workgroup (CUs x workgroups per CU from the occupancy query of the queue
-// variant) the queue variant on as many workgroups as are resident at once;
-// otherwise the plain variant, one workgroup per item (with few items per CU
-// the queue's draws and the lost XCD locality of later tickets cost more than
-// the balance gains: measured on configs 1 and 3).
-struct PersistentGrid {
-  static constexpr int kQueueMin = 4;
-  std::atomic<int> resident{0};
-  // Workgroups of the launch; *queue says which variant.
-  int64_t size(const void* queue_kern, int threads, int lds, int64_t items, bool* queue) {
-    int n = resident.load(std::memory_order_relaxed);
-    if (n == 0) {
-      int dev = 0, cus = 0, per_cu = 0;
-      if (hipGetDevice(&dev) != hipSuccess ||
-          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, queue_kern, threads, lds) !=
-              hipSuccess)
-        return 0;
-      n = cus * std::max(per_cu, 1);
-      resident.store(n, std::memory_order_relaxed);
-    }
-    *queue = items > (int64_t)kQueueMin * n;
-    return *queue ? n : items;
-  }
-};
 
 static hipError_t launch_dq_ds(const BwdParams& a, hipStream_t stream) {
   using C = DqDsCfg;

@@ -416,6 +416,17 @@ __device__ __forceinline__ int zigzag(int r, int n) {
   return (r & 1) ? (r >> 1) : (n - 1 - (r >> 1));
 }
 
+// Thread index as seen by one work item.  In a queue kernel (QUEUE) it passes
+// through an empty asm, so the per-lane offsets derived from it are formed in
+// each item rather than hoisted out of the ticket loop into registers held
+// across all items (which then spill inside the step loops).
+template <bool QUEUE>
+__device__ __forceinline__ int item_thread_id() {
+  int t = threadIdx.x;
+  if constexpr (QUEUE) asm volatile("" : "+v"(t));
+  return t;
+}
+
 // Work queue of a persistent launch (at most as many workgroups as are
 // resident at once, each taking tiles until they run out), so every CU stays
 // busy to the end however unevenly the tiles' costs or the hardware's

@@ -1,6 +1,8 @@
 // Kernel parameter blocks and launchers shared by the C ABI layer.
 #pragma once
 
+#include <atomic>
+
 #include "g4_common.h"
 
 namespace g4 {
@@ -58,6 +60,34 @@ size_t spans_bytes(const g4_problem& p);
 size_t delta_bytes(const g4_problem& p);
 size_t raise_flags_bytes(const g4_problem& p);
 constexpr size_t kSchedBytes = 256;  // work-queue counters (backward workspace tail)
+
+// Launch shape of a tile kernel with a work-queue variant: with more than
+// kQueueMin items per resident workgroup (CUs x workgroups per CU from the
+// occupancy query of the queue variant) the queue variant on as many
+// workgroups as are resident at once; otherwise the plain variant, one
+// workgroup per item (with few items per CU the queue's draws and the lost
+// XCD locality of later tickets cost more than the balance gains: measured on
+// configs 1 and 3).
+struct PersistentGrid {
+  static constexpr int kQueueMin = 4;
+  std::atomic<int> resident{0};
+  // Workgroups of the launch; *queue says which variant.
+  int64_t size(const void* queue_kern, int threads, int lds, int64_t items, bool* queue) {
+    int n = resident.load(std::memory_order_relaxed);
+    if (n == 0) {
+      int dev = 0, cus = 0, per_cu = 0;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, queue_kern, threads, lds) !=
+              hipSuccess)
+        return 0;
+      n = cus * (per_cu > 1 ? per_cu : 1);
+      resident.store(n, std::memory_order_relaxed);
+    }
+    *queue = items > (int64_t)kQueueMin * n;
+    return *queue ? n : items;
+  }
+};
 // dS buffer of the head-dim 512 causal backward (0: the dQ stage recomputes S, dP).
 size_t ds_bytes(const g4_problem& p);
 void ds_geometry(const g4_problem& p, int* rows, int* cols);
