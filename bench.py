@@ -177,7 +177,7 @@ def kernel_roofline(torch, g, tensors, *, s: int, reps: int):
     algo = {
         "fwd": ("mfma", 2.0 * hq * p * 2 * d),           # S, O
         "bwd_dkdv": ("mfma", 2.0 * hq * p * 4 * d),      # S, dP, dV, dK
-        "bwd_dq": ("mfma", 2.0 * hq * p * 3 * d),        # S, dP, dQ
+        "bwd_dq": ("mfma", 2.0 * hq * p * 1 * d),        # dQ from the dK/dV kernel's dS tiles
         "bwd_delta": ("hbm", 2.0 * s * hq * d * 2 + s * hq * 4),  # read O, dO; write delta
     }
     fns = {"fwd": st.forward, "bwd_delta": st.delta, "bwd_dkdv": st.dkdv, "bwd_dq": st.dq_stage}
