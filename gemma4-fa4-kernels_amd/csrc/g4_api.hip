@@ -5,6 +5,8 @@
 
 #include <string>
 
+#include <algorithm>
+
 #include "g4_kernels.h"
 
 namespace {
@@ -110,24 +112,42 @@ namespace g4 {
 size_t delta_bytes(const g4_problem& p) {
   return align256((size_t)q_stream_tokens(p) * p.num_q_heads * 4);
 }
-// dS tiles for the head-dim 512 causal backward: the dK/dV kernel writes each
-// step's dS (bf16) and the dQ stage is then a plain product dQ^T = K^T dS^T
-// instead of recomputing S and dP.  Used for text-causal problems (no window,
-// no bidirectional vision: every tile pair lies in the causal triangle of its
-// sequence) while the buffer stays within 16 GiB.
+// dS tiles written by the dK/dV kernel (bf16, one 4 KB tile [64 keys][32
+// queries] per (query head, 32-query row, 64-key tile)) so that the dQ stage
+// is a plain product dQ^T = K^T dS^T instead of recomputing S and dP.
+// - Head dim 512, text causal (no window, no bidirectional vision): dense over
+//   rows x key tiles; every visited pair lies in the causal triangle.
+// - Head dim 256 with a window: a band of ds_cols key tiles per row, starting
+//   at the tile of the row's first query's window start: (W + 30) / 64 + 2
+//   tiles cover every key the row's window and causal part admit, and with
+//   bidirectional vision up to 18 more (1152 keys) hold keys of vision spans
+//   that reach past the row's causal end, as far as the 16 GiB cap allows.
+//   The dQ stage recomputes the query tiles whose spans reach past the band.
+// Used while the buffer stays within 16 GiB.
+constexpr size_t kDsCap = size_t(16) << 30;
 void ds_geometry(const g4_problem& p, int* rows, int* cols) {
   const int64_t r = p.cu_seqlens_q ? p.total_q / 32 + p.num_seqs
                                    : (int64_t)p.num_seqs * ((p.seqlen_q + 31) / 32);
   *rows = (int)r;
-  *cols = (p.seqlen_k + 63) / 64;
+  if (p.head_dim == 256 && p.window > 0) {
+    const int base = (p.window + 30) / 64 + 2;
+    const bool vis = p.vision_ids != nullptr && p.bidirectional_vision;
+    const int64_t per_col = r * p.num_q_heads * 4096;
+    const int64_t fit = per_col > 0 ? (int64_t)kDsCap / per_col : base;
+    *cols = (int)std::max<int64_t>(base, std::min<int64_t>(base + (vis ? 18 : 0), fit));
+  } else {
+    *cols = (p.seqlen_k + 63) / 64;
+  }
 }
 size_t ds_bytes(const g4_problem& p) {
-  if (p.head_dim != 512 || p.window != 0 || (p.vision_ids != nullptr && p.bidirectional_vision))
-    return 0;
+  const bool dense = p.head_dim == 512 && p.window == 0 &&
+                     !(p.vision_ids != nullptr && p.bidirectional_vision);
+  const bool band = p.head_dim == 256 && p.window > 0;
+  if (!dense && !band) return 0;
   int rows, cols;
   ds_geometry(p, &rows, &cols);
   const size_t b = (size_t)rows * cols * p.num_q_heads * 4096;
-  return b <= (size_t(16) << 30) ? b : 0;
+  return b <= kDsCap ? b : 0;
 }
 // One int per (sequence, 32-query group, query head) for the head-dim 512
 // forward's second pass.

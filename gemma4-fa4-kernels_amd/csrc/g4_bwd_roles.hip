@@ -50,6 +50,42 @@ namespace g4 {
 namespace {
 
 
+// Head dim 256 with stored dS: the last key tile each 32-query row of the
+// 128-query tile at i0 reaches (its causal end, extended by the vision spans
+// of its queries; -1 for rows past the sequence), and whether some row reaches
+// past its stored band (such tiles are recomputed by dq_roles256_kernel).
+// `red` is four ints of LDS, free on entry.
+template <int NW>
+__device__ __forceinline__ bool dq_row_key_ends(const BwdParams& a, const Seq& sq, int i0,
+                                                int off, int tid, int* red, int (&kt_hi)[4]) {
+  const bool vis = a.p.vision_ids != nullptr && a.p.bidirectional_vision;
+  if (vis) {
+    // Waves 0 and 1 hold the tile's 128 queries: row = tid / 32.
+    int v = -1;
+    if (tid < 128 && i0 + tid < sq.lq) v = a.span_hi[sq.ktok + i0 + tid + off];
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+    barrier_lds();  // earlier readers of red are done
+    if (tid < 128 && (tid & 31) == 0) red[tid >> 5] = v;
+    barrier_lds();
+  }
+  bool need = false;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int r0 = i0 + 32 * g;
+    if (r0 >= sq.lq) {
+      kt_hi[g] = -1;
+      continue;
+    }
+    int last = min(r0 + 32, sq.lq) - 1 + off;
+    if (vis) last = max(last, red[g]);
+    kt_hi[g] = last / 64;
+    need |= kt_hi[g] - ds_band_first(r0 + off, a.p.window) >= a.ds_cols;
+  }
+  if (vis) barrier_lds();  // red may be overwritten after this
+  return need;
+}
+
 struct RolesCfg {
   static constexpr int D = 512;
   static constexpr int kNW = 8;
@@ -523,6 +559,7 @@ struct Roles256Kernel {
   int my_vid, my_doc;
   int grp, kvh, qt_lo, nqt;
   int64_t tq;
+  int64_t ds_row0;  // dS tile row of this sequence's first query tile
   RowReader<C::kCPR> rrd;
   TrReader<C::kCPR> trd;
   TileCopier<C::kCPR, C::kBM, 4> qcp, docp;  // Q by the P waves, dO by the dS waves
@@ -666,6 +703,26 @@ struct Roles256Kernel {
       for (int e = 0; e < 4; ++e)
         db[r4 >> 1][4 * (r4 & 1) + e] = (__bf16)(pv[e] * (dp[4 * r4 + e] - del4[e]));
     }
+    if (a->ds != nullptr) {
+      // This wave's 32 keys are one half of a 64-key dS tile of the step's
+      // query row; stored when the tile lies in the row's band.  The lane's
+      // key row holds four runs of four queries (rows 8 (r >> 2) + 4 h32 +
+      // (r & 3) of the accumulator layout).
+      int qh, i0;
+      coords(it, qh, i0);
+      const int c = (j0 + kb * 32) / 64 - ds_band_first(i0 + off, a->p.window);
+      if (c >= 0 && c < a->ds_cols) {
+        char* row = (char*)a->ds +
+                    (((int64_t)qh * a->ds_rows + ds_row0 + i0 / 32) * a->ds_cols + c) * 4096 +
+                    ((kb & 1) * 32 + (lane & 31)) * 64;
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int q4 = 0; q4 < 2; ++q4)
+            *(bf16x4*)(row + (8 * (2 * m + q4) + 4 * h32) * 2) =
+                bf16x4{db[m][4 * q4], db[m][4 * q4 + 1], db[m][4 * q4 + 2], db[m][4 * q4 + 3]};
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
     acc_step<0, 0>(qt, db);
     acc_step<1, 0>(qt, db);
@@ -770,6 +827,7 @@ __device__ __forceinline__ void dkdv_roles256_item(const BwdParams& a, char* sme
     ker.has_meta = ker.has_vid;
   }
   const int nsteps = ker.nqt * ker.grp;
+  ker.ds_row0 = sq.packed ? sq.qtok / 32 + ker.s : (int64_t)ker.s * ((p.seqlen_q + 31) / 32);
   const int jc = min(ker.my_j, sq.lk - 1);
   ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + jc] : -1;
   ker.my_doc = ker.has_doc ? p.document_ids[sq.ktok + jc] : 0;
@@ -1286,6 +1344,11 @@ __device__ __forceinline__ void dq_roles256_item(const BwdParams& a, char* smem_
   const int i0 = qt * C::kBM;
   if (i0 >= sq.lq) return;
   const int off = sq.lk - sq.lq;
+  if (a.dq_recompute_only) {
+    int kt_hi[4];
+    if (!dq_row_key_ends<C::kNW>(a, sq, i0, off, tid, (int*)(smem_raw + C::kLdsRed), kt_hi))
+      return;
+  }
   ker.a0 = i0 + off;
   const int a_last_valid = min(i0 + C::kBM, sq.lq) - 1 + off;
   ker.has_vid = META && p.vision_ids != nullptr && p.bidirectional_vision;
@@ -1399,8 +1462,9 @@ __global__ void __launch_bounds__(DqRoles256Cfg::kNT, 1) dq_roles256_kernel(BwdP
 // skipped.  One barrier per key tile (copies one tile ahead).
 // ===========================================================================
 
+template <int D_>
 struct DqDsCfg {
-  static constexpr int D = 512;
+  static constexpr int D = D_;
   static constexpr int kNW = 8;
   static constexpr int kNT = kNW * 64;
   static constexpr int kBM = 128;  // queries per workgroup (four tile rows)
@@ -1410,6 +1474,8 @@ struct DqDsCfg {
   static constexpr int kLdsK = 0;                    // [2 buf] K tiles
   static constexpr int kLdsDs = 2 * kKTile;          // [2 buf][4 rows] dS tiles
   static constexpr int kLdsBytes = kLdsDs + 2 * 4 * 4096;
+  static constexpr int kDW = D / 4;      // head dims per wave
+  static constexpr int kNBw = kDW / 32;  // 32-wide head-dim blocks per wave
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 };
 
@@ -1434,23 +1500,53 @@ struct PlainTrReader {
   }
 };
 
+// TrReader's transposing reads of NB consecutive 32-column blocks starting at
+// block B0 (runtime, wave-uniform): block B sits at chunk group B >> 2 with
+// its 4-chunk slot XORed by 64 (B & 3) bytes, so each block keeps its own pair
+// of per-lane bases (TrReader's column offset must be a multiple of 256
+// bytes, which a quarter of a 256-wide row is not).
+template <int CPR, int NB>
+struct BlockTrReader {
+  int base[NB][2];
+  __device__ __forceinline__ void init(int lane, int b0) {
+    TrReader<CPR> t;
+    t.init(lane, 0);
+#pragma unroll
+    for (int k = 0; k < NB; ++k)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        base[k][e] = (t.base[e] ^ (64 * ((b0 + k) & 3))) + 256 * ((b0 + k) >> 2);
+  }
+  template <int ROW0, int K>
+  __device__ __forceinline__ bf16x8 read(const char G4_LDS* tile) const {
+    constexpr int imm = ROW0 * CPR * 16;
+    bf16x4 lo = lds_read_tr<true>(tile + base[K][0] + imm);
+    bf16x4 hi = lds_read_tr<true>(tile + base[K][1] + imm);
+    return cat4(lo, hi);
+  }
+};
+
+// dS tile addressing for the two layouts (see BwdParams::ds): the tile of
+// workgroup row g (0..3) and key tile c is at base + g * row_stride +
+// (c - first[g]) * col_stride.
+template <int D>
 struct DqDsKernel {
-  using C = DqDsCfg;
+  using C = DqDsCfg<D>;
   char G4_LDS* smem;
   const BwdParams* a;
   Seq sq;
   int lane, wave, h32, dquart, qpair;
-  // Last key tile (-1: row past the sequence) of this wave's two tile rows and
-  // of the row whose dS tiles this wave copies.
-  int ktm0, ktm1, ktm_copy;
+  // Key-tile range [lo, hi] (hi = -1: row past the sequence) of this wave's
+  // two tile rows and of the row whose dS tiles this wave copies.
+  int lo0, hi0, lo1, hi1, lo_copy, hi_copy;
   const __bf16* kbase;
   int64_t kstride;
-  const char* ds_col0;  // dS tile of key tile 0, first tile row of this workgroup
+  const char* ds_copy_row;  // dS tile of key tile lo_copy in the copied row
   int64_t ds_col_stride;
-  TrReader<C::kCPR> trk;
+  BlockTrReader<C::kCPR, C::kNBw> trk;
   PlainTrReader trs;
   TileCopier<C::kCPR, C::kBN, C::kNW> kcp;
-  f32x16 acc[2][4];
+  f32x16 acc[2][C::kNBw];
 
   __device__ __forceinline__ void issue(int kt, int buf) {
     const int row0 = kt * C::kBN;
@@ -1458,8 +1554,8 @@ struct DqDsKernel {
                       smem + C::kLdsK + buf * C::kKTile);
     // dS: four 4 KB tiles, two 1 KB chunks per wave.
     const int g = wave >> 1;
-    if (kt <= ktm_copy) {
-      const char* src = ds_col0 + kt * ds_col_stride + g * 4096;
+    if (kt >= lo_copy && kt <= hi_copy) {
+      const char* src = ds_copy_row + (int64_t)(kt - lo_copy) * ds_col_stride;
       char G4_LDS* dst = smem + C::kLdsDs + (buf * 4 + g) * 4096;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -1472,29 +1568,33 @@ struct DqDsKernel {
   template <int KS>
   __device__ __forceinline__ void kstep(const char G4_LDS* kt_tile, const char G4_LDS* ds0,
                                         const char G4_LDS* ds1, bool v0, bool v1) {
-    const bf16x8 ak[4] = {trk.template read<16 * KS, 0, 0>(kt_tile),
-                          trk.template read<16 * KS, 0, 1>(kt_tile),
-                          trk.template read<16 * KS, 0, 2>(kt_tile),
-                          trk.template read<16 * KS, 0, 3>(kt_tile)};
+    bf16x8 ak[C::kNBw];
+    ak[0] = trk.template read<16 * KS, 0>(kt_tile);
+    ak[1] = trk.template read<16 * KS, 1>(kt_tile);
+    if constexpr (C::kNBw == 4) {
+      ak[2] = trk.template read<16 * KS, 2>(kt_tile);
+      ak[3] = trk.template read<16 * KS, 3>(kt_tile);
+    }
     if (v0) {
       const bf16x8 bs = trs.template read<16 * KS>(ds0);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) acc[0][b] = mfma32(ak[b], bs, acc[0][b]);
+      for (int b = 0; b < C::kNBw; ++b) acc[0][b] = mfma32(ak[b], bs, acc[0][b]);
     }
     if (v1) {
       const bf16x8 bs = trs.template read<16 * KS>(ds1);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) acc[1][b] = mfma32(ak[b], bs, acc[1][b]);
+      for (int b = 0; b < C::kNBw; ++b) acc[1][b] = mfma32(ak[b], bs, acc[1][b]);
     }
   }
 };
 
+
 // Work item L: query tile (last, i.e. heaviest under the causal mask, first),
 // then sequence, then query head.
-template <bool QUEUE>
+template <int D, bool QUEUE>
 __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, int L) {
-  using C = DqDsCfg;
-  DqDsKernel ker;
+  using C = DqDsCfg<D>;
+  DqDsKernel<D> ker;
   ker.smem = (char G4_LDS*)smem_raw;
   ker.a = &a;
   const g4_problem& p = a.p;
@@ -1518,44 +1618,68 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
   const int i0 = qt * C::kBM;
   if (i0 >= sq.lq) return;
   const int off = sq.lk - sq.lq;
-  auto kt_last = [&](int g) {
-    const int r0 = i0 + 32 * g;
-    return r0 < sq.lq ? (min(r0 + 32, sq.lq) - 1 + off) / C::kBN : -1;
+  constexpr bool kBand = D == 256;
+  // Key tiles of row g: up to the causal end of its last query (for the band,
+  // extended by its queries' vision spans) and, for the band, from the band
+  // start of its first query.
+  int kt_hi[4];
+  if constexpr (kBand) {
+    if (dq_row_key_ends<C::kNW>(a, sq, i0, off, tid, (int*)smem_raw, kt_hi)) return;
+  } else {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int r0 = i0 + 32 * g;
+      kt_hi[g] = r0 < sq.lq ? (min(r0 + 32, sq.lq) - 1 + off) / C::kBN : -1;
+    }
+  }
+  auto kt_last = [&](int g) { return kt_hi[g]; };
+  auto kt_first = [&](int g) {
+    return kBand ? ds_band_first(i0 + 32 * g + off, p.window) : 0;
   };
+  const int kt_begin = kt_first(0);
   const int nkt = max(max(kt_last(0), kt_last(1)), max(kt_last(2), kt_last(3))) + 1;
-  ker.ktm0 = kt_last(2 * ker.qpair);
-  ker.ktm1 = kt_last(2 * ker.qpair + 1);
-  ker.ktm_copy = kt_last(ker.wave >> 1);
+  ker.lo0 = kt_first(2 * ker.qpair);
+  ker.hi0 = kt_last(2 * ker.qpair);
+  ker.lo1 = kt_first(2 * ker.qpair + 1);
+  ker.hi1 = kt_last(2 * ker.qpair + 1);
+  const int gc = ker.wave >> 1;
+  ker.lo_copy = kt_first(gc);
+  ker.hi_copy = kt_last(gc);
 
   ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
   ker.kstride = a.kl.token_stride;
   const int64_t row0 =
       (sq.packed ? sq.qtok / 32 + s : (int64_t)s * ((p.seqlen_q + 31) / 32)) + i0 / 32;
-  ker.ds_col_stride = (int64_t)a.ds_rows * 4096;
-  ker.ds_col0 = (const char*)a.ds + ((int64_t)qh * a.ds_cols * a.ds_rows + row0) * 4096;
-  ker.trk.init(ker.lane, ker.dquart * 128 * 2);
+  if constexpr (kBand) {
+    ker.ds_col_stride = 4096;
+    ker.ds_copy_row = (const char*)a.ds + (((int64_t)qh * a.ds_rows + row0 + gc) * a.ds_cols) * 4096;
+  } else {
+    ker.ds_col_stride = (int64_t)a.ds_rows * 4096;
+    ker.ds_copy_row = (const char*)a.ds + ((int64_t)qh * a.ds_cols * a.ds_rows + row0 + gc) * 4096;
+  }
+  ker.trk.init(ker.lane, ker.dquart * C::kNBw);
   ker.trs.init(ker.lane);
   ker.kcp.init(ker.kstride, ker.wave, ker.lane);
 #pragma unroll
   for (int g = 0; g < 2; ++g)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) ker.acc[g][b] = f32x16{};
+    for (int b = 0; b < C::kNBw; ++b) ker.acc[g][b] = f32x16{};
 
   const int g0 = 2 * ker.qpair;
-  if (nkt > 0) ker.issue(0, 0);
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int cur = kt & 1;
+  if (kt_begin < nkt) ker.issue(kt_begin, 0);
+  for (int kt = kt_begin; kt < nkt; ++kt) {
+    const int cur = (kt - kt_begin) & 1;
     vm_wait<0>();
     barrier_lds();  // tile kt landed; every wave is done with buffer cur ^ 1
     if (kt + 1 < nkt) ker.issue(kt + 1, cur ^ 1);
     const char G4_LDS* ktile = ker.smem + C::kLdsK + cur * C::kKTile;
     const char G4_LDS* ds0 = ker.smem + C::kLdsDs + (cur * 4 + g0) * 4096;
     const char G4_LDS* ds1 = ds0 + 4096;
-    const bool v0 = kt <= ker.ktm0, v1 = kt <= ker.ktm1;
-    ker.kstep<0>(ktile, ds0, ds1, v0, v1);
-    ker.kstep<1>(ktile, ds0, ds1, v0, v1);
-    ker.kstep<2>(ktile, ds0, ds1, v0, v1);
-    ker.kstep<3>(ktile, ds0, ds1, v0, v1);
+    const bool v0 = kt >= ker.lo0 && kt <= ker.hi0, v1 = kt >= ker.lo1 && kt <= ker.hi1;
+    ker.template kstep<0>(ktile, ds0, ds1, v0, v1);
+    ker.template kstep<1>(ktile, ds0, ds1, v0, v1);
+    ker.template kstep<2>(ktile, ds0, ds1, v0, v1);
+    ker.template kstep<3>(ktile, ds0, ds1, v0, v1);
   }
 
 #pragma unroll
@@ -1564,10 +1688,10 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
     if (my_i >= sq.lq) continue;
     __bf16* row = a.dq + tok_off(sq, s, sq.qtok, my_i, a.dql) + (int64_t)qh * a.dql.head_stride;
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < C::kNBw; ++b)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        const int d = ker.dquart * 128 + b * 32 + 8 * r4 + 4 * ker.h32;
+        const int d = ker.dquart * C::kDW + b * 32 + 8 * r4 + 4 * ker.h32;
         const f32x16& x = ker.acc[g2][b];
         *(bf16x4*)(row + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
                                      (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
@@ -1575,10 +1699,10 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
   }
 }
 
-// Persistent: a few workgroups per CU take query-tile tickets from the dQ
-// work queue, the heaviest tiles first.
-template <bool QUEUE>
-__global__ void __launch_bounds__(DqDsCfg::kNT, 1) dq_ds_kernel(BwdParams a) {
+// Persistent (QUEUE): a few workgroups per CU take query-tile tickets from
+// the dQ work queue, the heaviest tiles first.
+template <int D, bool QUEUE>
+__global__ void __launch_bounds__(DqDsCfg<D>::kNT, 1) dq_ds_kernel(BwdParams a) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   if constexpr (QUEUE) {
     const int n = a.num_seqs * a.ntiles * a.p.num_q_heads;
@@ -1586,18 +1710,19 @@ __global__ void __launch_bounds__(DqDsCfg::kNT, 1) dq_ds_kernel(BwdParams a) {
     for (;;) {
       const int t = wq.next((int G4_LDS*)smem_raw);
       if (t >= n) break;
-      dq_ds_item<true>(a, smem_raw, t);
+      dq_ds_item<D, true>(a, smem_raw, t);
     }
   } else {
-    dq_ds_item<false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
+    dq_ds_item<D, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
   }
 }
 
 }  // namespace
 
 
+template <int D>
 static hipError_t launch_dq_ds(const BwdParams& a, hipStream_t stream) {
-  using C = DqDsCfg;
+  using C = DqDsCfg<D>;
   static bool done[2] = {false, false};
   BwdParams b = a;
   b.ntiles = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
@@ -1605,9 +1730,10 @@ static hipError_t launch_dq_ds(const BwdParams& a, hipStream_t stream) {
   if (items <= 0) return hipSuccess;
   static PersistentGrid grid;
   bool queue = false;
-  const int64_t nblocks = grid.size((const void*)dq_ds_kernel<true>, C::kNT, C::kLdsBytes, items, &queue);
+  const int64_t nblocks =
+      grid.size((const void*)dq_ds_kernel<D, true>, C::kNT, C::kLdsBytes, items, &queue);
   if (nblocks <= 0) return hipErrorInvalidValue;
-  void (*kern)(BwdParams) = queue ? dq_ds_kernel<true> : dq_ds_kernel<false>;
+  void (*kern)(BwdParams) = queue ? dq_ds_kernel<D, true> : dq_ds_kernel<D, false>;
   if (!done[queue]) {
     hipError_t e = hipFuncSetAttribute((const void*)kern,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
@@ -1654,12 +1780,20 @@ hipError_t launch_dq_roles_d(const BwdParams& a, hipStream_t stream) {
 }
 
 hipError_t launch_bwd_dq(const BwdParams& a, hipStream_t stream) {
+  // With the dK/dV kernel's dS tiles in the workspace, dQ is a plain product.
   if (a.p.head_dim == 512) {
-    // With the dK/dV kernel's dS tiles in the workspace, dQ is a plain product.
-    if (a.ds != nullptr) return launch_dq_ds(a, stream);
+    if (a.ds != nullptr) return launch_dq_ds<512>(a, stream);
     return launch_dq_roles_d<512>(a, stream);
   }
-  if (a.p.head_dim == 256) return launch_dq_roles_d<256>(a, stream);
+  if (a.p.head_dim == 256) {
+    if (a.ds == nullptr) return launch_dq_roles_d<256>(a, stream);
+    hipError_t e = launch_dq_ds<256>(a, stream);
+    if (e != hipSuccess || a.p.vision_ids == nullptr || !a.p.bidirectional_vision) return e;
+    // Query tiles with vision spans past the stored band: recomputed.
+    BwdParams b = a;
+    b.dq_recompute_only = 1;
+    return launch_dq_roles_d<256>(b, stream);
+  }
   return hipErrorInvalidValue;
 }
 

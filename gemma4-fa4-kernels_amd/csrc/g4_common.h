@@ -357,6 +357,12 @@ __device__ __forceinline__ void issue_key_meta(const g4_problem& p, const Seq& s
   if (doc) g2l4(p.document_ids + idx, dst + 256);
 }
 
+// First key tile (64 keys) of the stored-dS band of the 32-query row whose
+// first query sits at key position a_first (window W > 0).
+__device__ __forceinline__ int ds_band_first(int a_first, int window) {
+  return max(a_first - window + 1, 0) / 64;
+}
+
 // Tokens in the Q stream (packed total, or num_seqs * seqlen_q).
 __device__ __forceinline__ int64_t q_stream_tokens_dev(const g4_problem& p) {
   return p.cu_seqlens_q ? p.total_q : (int64_t)p.num_seqs * p.seqlen_q;

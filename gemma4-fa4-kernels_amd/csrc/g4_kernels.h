@@ -44,12 +44,18 @@ struct BwdParams {
   const int* span_hi;
   int num_seqs;
   int ntiles;          // row tiles per sequence (set by the launchers)
-  // dS tiles of the head-dim 512 causal backward (null when not used): tile
-  // (query head h, key tile c, row r) at ((h * ds_cols + c) * ds_rows + r) * 4 KB,
-  // [64 keys][32 queries] bf16.  Row r of packed sequence s, query tile t is
-  // floor(cu_q[s] / 32) + s + t (fixed layouts: s * ceil(Sq / 32) + t).
+  // dS tiles written by the dK/dV kernel for the dQ stage (null when not used).
+  // Row r of packed sequence s, query tile t is floor(cu_q[s] / 32) + s + t
+  // (fixed layouts: s * ceil(Sq / 32) + t).  Head dim 512: tile (query head h,
+  // key tile c, row r) at ((h * ds_cols + c) * ds_rows + r) * 4 KB.  Head dim
+  // 256 (band): tile (h, r, key tile c) at ((h * ds_rows + r) * ds_cols +
+  // c - ds_band_first(r)) * 4 KB for c - ds_band_first(r) < ds_cols.  Each tile
+  // is [64 keys][32 queries] bf16.
   __bf16* ds;
   int ds_rows, ds_cols;
+  // Head dim 256 dQ after the stored-dS pass: only the query tiles whose vision
+  // spans reach past the stored band (set by the launcher).
+  int dq_recompute_only;
   // Work-queue ticket counters of the persistent tile kernels: [0] dK/dV,
   // [2] dQ; zeroed by the delta pass, and by each launch's last draw.
   unsigned* sched;

@@ -123,10 +123,18 @@ def test_forward_is_bitwise_repeatable_on_a_side_stream():
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
 
 
-def _raise_flags(st, nseg, max_q):
-    """The d512 forward's per-(segment, 32-query group, head) raise flags (workspace head)."""
-    n = nseg * ((max_q + 31) // 32) * 32
-    return st.ws[: 4 * n].view(torch.int32).cpu()
+def _raise_flags(st, nseg, max_q, lq=None):
+    """The d512 forward's per-(segment, 32-query group, head) raise flags (workspace head).
+
+    Only the groups inside each segment (lengths lq) are written by the kernels;
+    the slots past a shorter segment's end are never read and hold whatever the
+    workspace held before.
+    """
+    nq32 = (max_q + 31) // 32
+    flags = st.ws[: 4 * nseg * nq32 * 32].view(torch.int32).cpu().view(nseg, nq32, 32)
+    if lq is None:
+        return flags.flatten()
+    return torch.cat([flags[s, : (n + 31) // 32].flatten() for s, n in enumerate(lq)])
 
 
 @pytest.mark.parametrize("lq,lk", [([300, 450], [300, 450]), ([130], [700])])
@@ -148,7 +156,7 @@ def test_global_rescaling_pass_for_large_score_jumps(lq, lk):
     st = ops.Stages(plan, qd, kd, vd, torch.zeros_like(qd))
     st.forward()
     torch.cuda.synchronize()
-    assert int(_raise_flags(st, len(lq), max(lq)).sum()) > 0, "no row took the rescaling pass"
+    assert int(_raise_flags(st, len(lq), max(lq), lq).sum()) > 0, "no row took the rescaling pass"
     o_ref, l_ref, *_ = oracle_fwd_bwd(q, k, v, cq, ck, window=None)
     check_forward(st.o, st.lse, o_ref, l_ref, local=False, label=f"global rescale {lq}/{lk}")
     o2, lse2 = g.fa4_global_varlen_forward_only(qd, kd, vd, cq.to(DEV), ck.to(DEV),
