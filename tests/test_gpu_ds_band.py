@@ -1,0 +1,54 @@
+"""Head-dim 256 backward with stored dS: the band and its recompute routing.
+
+The local dK/dV kernel stores dS tiles in a band of key tiles per 32-query
+row (window and causal part plus up to 18 tiles of vision spans); the dQ
+stage takes the product over stored tiles for query tiles that stay inside
+their band and recomputes the others.  A 1500-token vision block starting
+past the first window reaches beyond the band of its first rows (those query
+tiles are recomputed) but not of its later rows; documents are added on a
+second segment.  Compared with the fp64 oracle through the C ABI stages.
+"""
+
+import pytest
+import torch
+
+from g4_testutil import check_forward, check_gradients, cu, qkv
+from oracle.attention import attention_fwd_bwd, bf16_baseline_fwd_bwd
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def test_long_vision_block_reaches_past_the_band():
+    import gemma4_fa4_amd as g
+    from gemma4_fa4_amd import ops
+    from gemma4_fa4_amd.attention import _packed_plan
+
+    lens = [3000, 700]
+    t = sum(lens)
+    q, k, v, do, dlse = qkv(777, t, t, 32, 16, 256)
+    vis = torch.full((t,), -1, dtype=torch.int32)
+    vis[1100:2600] = 0          # 1500 tokens: rows near 1100 reach past their band
+    vis[3000 + 100:3000 + 180] = 1
+    docs = torch.zeros(t, dtype=torch.int32)
+    docs[3000 + 400:] = 1       # second segment: two documents, the block in the first
+    c = cu(lens)
+    plan = _packed_plan(q.to(DEV), k.to(DEV), c.to(DEV), c.to(DEV), max(lens), max(lens),
+                        g.SLIDING_ATTENTION, vision=vis.to(DEV), documents=docs.to(DEV))
+    st = ops.Stages(plan, q.to(DEV), k.to(DEV), v.to(DEV), do.to(DEV), dlse.to(DEV))
+    st.forward()
+    st.delta()
+    st.dkdv()
+    st.dq_stage()
+    torch.cuda.synchronize()
+    args = dict(sliding_window=1024, vision_block_ids=vis.to(DEV), document_ids=docs.to(DEV),
+                allow_vision_bidirectional=True)
+    o, lse, dq, dk, dv = attention_fwd_bwd(
+        q.to(DEV), k.to(DEV), v.to(DEV), c.tolist(), c.tolist(), do=do.to(DEV),
+        dlse=dlse.to(DEV), compute_dtype=torch.float64, **args)
+    _, bq, bk, bv = bf16_baseline_fwd_bwd(
+        q.to(DEV), k.to(DEV), v.to(DEV), c.tolist(), c.tolist(), do=do.to(DEV),
+        dlse=dlse.to(DEV), **args)
+    check_forward(st.o, st.lse, o.cpu(), lse.cpu(), local=True, label="band")
+    check_gradients([st.dq, st.dk, st.dv], [x.cpu() for x in (dq, dk, dv)],
+                    [x.cpu() for x in (bq, bk, bv)], label="band")
