@@ -135,9 +135,10 @@ int g4_attn_bwd_delta(const g4_problem* p,
                       void* stream);
 
 /* Stage 2: dK, dV (KV-tile major, reduces the GQA group on chip).  Needs the
- * workspace left by g4_attn_bwd_delta; for head dim 512 causal text problems
- * it also stores dS there for g4_attn_bwd_dq.  Replaces the dKV-only FA4
- * launches (patch 0002:1347-1418) and FA4's fused local backward dK/dV. */
+ * workspace left by g4_attn_bwd_delta; it also stores dS tiles there for
+ * g4_attn_bwd_dq (head dim 512 causal text problems, and head dim 256 with a
+ * window).  Replaces the dKV-only FA4 launches (patch 0002:1347-1418) and
+ * FA4's fused local backward dK/dV. */
 int g4_attn_bwd_dkdv(const g4_problem* p,
                      const void* q, g4_layout q_layout,
                      const void* k, g4_layout k_layout,
@@ -150,10 +151,9 @@ int g4_attn_bwd_dkdv(const g4_problem* p,
                      void* stream);
 
 /* Stage 3: dQ (Q-tile major).  Needs the workspace left by
- * g4_attn_bwd_delta and, for head dim 512 causal text problems, by
- * g4_attn_bwd_dkdv (the dS tiles it stores there; dQ is then one product
- * over them).  Replaces the D256-stream dQ-only FA4 launches
- * (patch 0002:1367-1381, 1430-1449). */
+ * g4_attn_bwd_delta and, where g4_attn_bwd_dkdv stored dS tiles there, by
+ * that stage (dQ is then one product over them).  Replaces the D256-stream
+ * dQ-only FA4 launches (patch 0002:1367-1381, 1430-1449). */
 int g4_attn_bwd_dq(const g4_problem* p,
                    const void* q, g4_layout q_layout,
                    const void* k, g4_layout k_layout,
