@@ -529,7 +529,9 @@ def _free_hbm(device) -> int:
 
 
 def _preflight_metadata_workspace(plan: _Plan, device) -> None:
-    required = plan.workspace_bytes(1)
+    # The forward's workspace: the vision-span tables (and raise flags).  The
+    # backward's delta and dS tiles are budgeted by _preflight_backward.
+    required = plan.workspace_bytes(0)
     if required > _METADATA_WORKSPACE_MAX_BYTES:
         raise UnsupportedMI355XPath(
             f"vision-span workspace requires {required} bytes, above the 2 GiB safety limit"
