@@ -19,7 +19,7 @@ differentiable.  Queries are the lower-right suffix of their key sequence.
 from __future__ import annotations
 
 import ctypes
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
@@ -182,6 +182,49 @@ def _prepare_vision_block_ids(vision_block_ids: torch.Tensor, q: torch.Tensor) -
     return _normalize_int32_metadata(vision_block_ids, name="vision_block_ids").view(-1)
 
 
+class _CumulativeCheck:
+    """The checks that need the values of ``cu_seqlens``, run just before the first launch.
+
+    Reading the arrays is a device-to-host copy, which waits for all earlier
+    work on the stream; the reference reads them while validating
+    (h100.py:351-352, 1122-1123), so the GPU sits idle for every host step
+    that follows.  Here the steps that do not need the values (the checks the
+    reference takes after the read, the plan, the HBM preflight, output
+    allocation) run first, while the GPU is still busy, and the read happens
+    immediately before the launch.  An error from such a step is held back
+    until the length checks have passed, so every input raises the error the
+    reference's order gives it.
+    """
+
+    def __init__(self, lengths):
+        self._lengths = lengths
+        self._held: Exception | None = None
+        self._settled = False
+
+    def later(self, step, *args):
+        """Run a step the reference takes after the length checks; hold its error."""
+        if self._held is not None:
+            return None
+        try:
+            return step(*args)
+        except Exception as exc:  # re-raised by settle(), after the length checks
+            self._held = exc
+            return None
+
+    @property
+    def failed(self) -> bool:
+        return self._held is not None
+
+    def settle(self) -> None:
+        """Read the arrays, check the lengths, then raise any held error."""
+        if self._settled:
+            return
+        self._settled = True
+        self._lengths()
+        if self._held is not None:
+            raise self._held
+
+
 def _cumulative_lengths(cu_q, cu_k, q, k, *, label: str):
     # One device-to-host copy (and stream sync) for both arrays.
     if cu_q.data_ptr() == cu_k.data_ptr() and cu_q.shape == cu_k.shape:
@@ -244,14 +287,18 @@ def _validate_local_varlen(q, k, v, cu_q, cu_k, max_q, max_k, spec, *, require_d
         raise UnsupportedMI355XPath("varlen local attention requires 1 <= max Sq <= max Sk <= 262144")
     if max_q > max_k:
         raise UnsupportedMI355XPath("varlen local attention requires max Sq <= max Sk")
-    q_lengths, k_lengths = _cumulative_lengths(cu_q, cu_k, q, k, label="packed")
-    if any(lq > lk for lq, lk in zip(q_lengths, k_lengths)):
-        raise UnsupportedMI355XPath("each packed sequence requires Sq <= Sk")
-    if max(q_lengths) != max_q or max(k_lengths) != max_k:
-        raise ValueError("max_seqlen_q/max_seqlen_k must equal the cumulative maxima")
+
+    def lengths():
+        q_lengths, k_lengths = _cumulative_lengths(cu_q, cu_k, q, k, label="packed")
+        if any(lq > lk for lq, lk in zip(q_lengths, k_lengths)):
+            raise UnsupportedMI355XPath("each packed sequence requires Sq <= Sk")
+        if max(q_lengths) != max_q or max(k_lengths) != max_k:
+            raise ValueError("max_seqlen_q/max_seqlen_k must equal the cumulative maxima")
+
+    check = _CumulativeCheck(lengths)
     if require_device:
-        _require_gfx950(q.device)
-    return q_lengths, k_lengths
+        check.later(_require_gfx950, q.device)
+    return check
 
 
 def _prepare_packed_k_metadata(values, k: torch.Tensor, *, name: str):
@@ -325,15 +372,23 @@ def _validate_global_varlen(q, k, v, cu_q, cu_k, max_q, max_k, spec, *, allow_ba
             "global packed forward-only cannot participate in autograd; use "
             "fa4_global_varlen_forward"
         )
-    q_lengths, k_lengths = _cumulative_lengths(cu_q, cu_k, q, k, label="global packed")
-    if any(lq > lk for lq, lk in zip(q_lengths, k_lengths)):
-        raise UnsupportedMI355XPath("global packed segments require 0 <= Sq <= Sk per segment")
-    if max(q_lengths) != max_q or max(k_lengths) != max_k:
-        raise ValueError("global packed maxima must equal the cumulative segment maxima")
+
+    def lengths():
+        q_lengths, k_lengths = _cumulative_lengths(cu_q, cu_k, q, k, label="global packed")
+        if any(lq > lk for lq, lk in zip(q_lengths, k_lengths)):
+            raise UnsupportedMI355XPath("global packed segments require 0 <= Sq <= Sk per segment")
+        if max(q_lengths) != max_q or max(k_lengths) != max_k:
+            raise ValueError("global packed maxima must equal the cumulative segment maxima")
+
+    check = _CumulativeCheck(lengths)
+    check.later(_require_int32_totals, q, k)
+    check.later(_require_gfx950, q.device)
+    return check
+
+
+def _require_int32_totals(q, k) -> None:
     if q.shape[0] > torch.iinfo(torch.int32).max or k.shape[0] > torch.iinfo(torch.int32).max:
         raise UnsupportedMI355XPath("packed global totals must fit signed INT32")
-    _require_gfx950(q.device)
-    return q_lengths, k_lengths
 
 
 # ---------------------------------------------------------------------------
@@ -370,6 +425,13 @@ class _Plan:
     cu_k: torch.Tensor | None = None
     vision: torch.Tensor | None = None
     documents: torch.Tensor | None = None
+    # Cumulative-array checks still to run before the first launch.
+    pending: _CumulativeCheck | None = field(default=None, repr=False, compare=False)
+
+    def _settle(self) -> None:
+        pending, self.pending = self.pending, None
+        if pending is not None:
+            pending.settle()
 
     def problem(self) -> G4Problem:
         p = G4Problem()
@@ -412,14 +474,18 @@ class _Plan:
         return torch.empty(max(self.workspace_bytes(phase), 256), dtype=torch.uint8, device=device)
 
     def forward(self, q, k, v):
-        lib = _lib.load()
-        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-        lse = torch.empty(self.lse_shape(), dtype=torch.float32, device=q.device)
-        ws = self._workspace(0, q.device)
+        try:
+            lib = _lib.load()
+            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+            lse = torch.empty(self.lse_shape(), dtype=torch.float32, device=q.device)
+            ws = self._workspace(0, q.device)
+        except Exception:
+            self._settle()  # an invalid cu_seqlens is reported first
+            raise
         prob = self.problem()
         with torch.cuda.device(q.device):
             stream = torch.cuda.current_stream(q.device).cuda_stream
-            rc = lib.g4_attn_fwd(
+            args = (
                 ctypes.byref(prob),
                 q.data_ptr(), _layout(q, self.packed),
                 k.data_ptr(), _layout(k, self.packed),
@@ -427,6 +493,8 @@ class _Plan:
                 out.data_ptr(), _layout(out, self.packed),
                 lse.data_ptr(), ws.data_ptr(), ws.numel(), stream,
             )
+            self._settle()
+            rc = lib.g4_attn_fwd(*args)
         _lib.check(rc)
         return out, lse
 
@@ -588,6 +656,15 @@ def _run(q, k, v, plan: _Plan):
     return plan.forward(q, k, v)
 
 
+def _run_checked(q, k, v, check: _CumulativeCheck, prepare, *, autograd: bool = True):
+    """Build the plan while the GPU is busy; the cumulative arrays are read at launch."""
+    plan = check.later(prepare)
+    if check.failed:
+        check.settle()  # raises: the length checks' error, else the held one
+    plan.pending = check
+    return _run(q, k, v, plan) if autograd else plan.forward(q, k, v)
+
+
 # ---------------------------------------------------------------------------
 # public adapters (reference names; h100.py:750-1394)
 # ---------------------------------------------------------------------------
@@ -638,16 +715,22 @@ def fa4_local_varlen_forward(
     segment; the device scheduler bounds each tile's key range from the window
     and the vision spans (no host schedule, no per-segment launches).
     """
-    _validate_local_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec)
-    vision = _prepare_packed_k_metadata(vision_block_ids, k, name="vision_block_ids")
-    documents = _prepare_packed_k_metadata(document_ids, k, name="document_ids")
-    plan = _packed_plan(
-        q, k, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec,
-        vision=vision, documents=documents,
+    check = _validate_local_varlen(
+        q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec
     )
-    if vision is not None:
-        _preflight_metadata_workspace(plan, q.device)
-    return _run(q, k, v, plan)
+
+    def prepare():
+        vision = _prepare_packed_k_metadata(vision_block_ids, k, name="vision_block_ids")
+        documents = _prepare_packed_k_metadata(document_ids, k, name="document_ids")
+        plan = _packed_plan(
+            q, k, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec,
+            vision=vision, documents=documents,
+        )
+        if vision is not None:
+            _preflight_metadata_workspace(plan, q.device)
+        return plan
+
+    return _run_checked(q, k, v, check, prepare)
 
 
 def fa4_global_forward_only(q, k, v, *, spec: AttentionLayerSpec = GLOBAL_ATTENTION):
@@ -669,10 +752,15 @@ def fa4_global_varlen_forward_only(
     spec: AttentionLayerSpec = GLOBAL_ATTENTION,
 ):
     """Packed lower-right global d512 forward without autograd."""
-    _validate_global_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec)
-    _preflight_forward_outputs(q)
-    plan = _packed_plan(q, k, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec)
-    return plan.forward(q, k, v)
+    check = _validate_global_varlen(
+        q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec
+    )
+
+    def prepare():
+        _preflight_forward_outputs(q)
+        return _packed_plan(q, k, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec)
+
+    return _run_checked(q, k, v, check, prepare, autograd=False)
 
 
 def fa4_global_varlen_forward(
@@ -687,16 +775,20 @@ def fa4_global_varlen_forward(
     spec: AttentionLayerSpec = GLOBAL_ATTENTION,
 ):
     """Packed global d512 forward with the atomic-free MI355X backward."""
-    _validate_global_varlen(
+    check = _validate_global_varlen(
         q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec,
         allow_backward=True,
     )
-    plan = _packed_plan(q, k, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec)
-    if _requires_backward(q, k, v):
-        _preflight_backward(plan, q, k, v)
-    else:
-        _preflight_forward_outputs(q)
-    return _run(q, k, v, plan)
+
+    def prepare():
+        plan = _packed_plan(q, k, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec)
+        if _requires_backward(q, k, v):
+            _preflight_backward(plan, q, k, v)
+        else:
+            _preflight_forward_outputs(q)
+        return plan
+
+    return _run_checked(q, k, v, check, prepare)
 
 
 def fa4_global_text_forward(q, k, v, *, spec: AttentionLayerSpec = GLOBAL_ATTENTION):

@@ -162,6 +162,56 @@ def test_global_backward_budget_fails_closed():
         att._check_global_backward_budget(budget + 1, free)
 
 
+def _global_packed(lengths=(3, 2)):
+    s = g.GLOBAL_ATTENTION
+    t = sum(lengths)
+    q = torch.zeros(t, s.num_q_heads, 512, dtype=torch.bfloat16)
+    k = torch.ones(t, s.num_kv_heads, 512, dtype=torch.bfloat16)
+    v = torch.full_like(k, 2)
+    cu = torch.tensor([0, *torch.tensor(lengths).cumsum(0).tolist()], dtype=torch.int32)
+    return q, k, v, cu
+
+
+def test_cumulative_arrays_are_read_at_launch(monkeypatch):
+    """The cu_seqlens read (a stream sync) follows the preflight and the allocation."""
+    monkeypatch.setattr(att, "_require_gfx950", lambda _device: None)
+    calls = []
+    real = att._cumulative_lengths
+    monkeypatch.setattr(att, "_cumulative_lengths",
+                        lambda *a, **kw: (calls.append("read"), real(*a, **kw))[1])
+    monkeypatch.setattr(att, "_preflight_forward_outputs", lambda _q: calls.append("preflight"))
+
+    def no_library():
+        calls.append("load")
+        raise g.UnsupportedMI355XPath("library withheld by the test")
+
+    monkeypatch.setattr(_lib, "load", no_library)
+    q, k, v, cu = _global_packed()
+    with pytest.raises(g.UnsupportedMI355XPath, match="withheld"):
+        g.fa4_global_varlen_forward_only(q, k, v, cu, cu, max_seqlen_q=3, max_seqlen_k=3)
+    assert calls == ["preflight", "load", "read"]
+    # Invalid arrays still report their own error before the later failure.
+    calls.clear()
+    with pytest.raises(ValueError, match="maxima"):
+        g.fa4_global_varlen_forward_only(q, k, v, cu, cu, max_seqlen_q=4, max_seqlen_k=4)
+    assert calls == ["preflight", "load", "read"]
+
+
+def test_held_errors_follow_the_length_checks(monkeypatch):
+    monkeypatch.setattr(att, "_require_gfx950", lambda _device: None)
+
+    def refuse(_q):
+        raise g.UnsupportedMI355XPath("preflight refused by the test")
+
+    monkeypatch.setattr(att, "_preflight_forward_outputs", refuse)
+    q, k, v, cu = _global_packed()
+    bad = torch.tensor([0, 4, 5], dtype=torch.int32)
+    with pytest.raises(ValueError, match="maxima"):
+        g.fa4_global_varlen_forward_only(q, k, v, bad, bad, max_seqlen_q=3, max_seqlen_k=3)
+    with pytest.raises(g.UnsupportedMI355XPath, match="refused by the test"):
+        g.fa4_global_varlen_forward_only(q, k, v, cu, cu, max_seqlen_q=3, max_seqlen_k=3)
+
+
 def test_model_contract_constants():
     s, f = g.SLIDING_ATTENTION, g.GLOBAL_ATTENTION
     assert (s.head_dim_qk, s.num_q_heads, s.num_kv_heads, s.sliding_window) == (256, 32, 16, 1024)
