@@ -86,6 +86,58 @@ __device__ __forceinline__ bool dq_row_key_ends(const BwdParams& a, const Seq& s
   return need;
 }
 
+// The two MFMA products of the role kernels with kAhead LDS operand reads in
+// flight: read n + kAhead is issued right after MFMA n and sched_barrier pins
+// that order.  Left to itself the scheduler falls back to one read per MFMA,
+// each waited for, at the register budget of two waves per SIMD.
+constexpr int kAhead = 2;
+
+// acc[B] += (tile^T rows 16 M ...)[32 x 16] . b[M], over M in {0, 1}, B in [0, NB).
+template <int NB, int N, class TR>
+__device__ __forceinline__ void acc_pipe(const TR& trd, const char G4_LDS* t,
+                                         const bf16x8 (&b)[2], f32x16 (&acc)[NB],
+                                         bf16x8 (&x)[kAhead]) {
+  if constexpr (N < 2 * NB) {
+    acc[N % NB] = mfma32(x[N % kAhead], b[N / NB], acc[N % NB]);
+    if constexpr (N + kAhead < 2 * NB)
+      x[N % kAhead] = trd.template read<16 * ((N + kAhead) / NB), 0, (N + kAhead) % NB>(t);
+    __builtin_amdgcn_sched_barrier(0);
+    acc_pipe<NB, N + 1>(trd, t, b, acc, x);
+  }
+}
+template <int NB, class TR>
+__device__ __forceinline__ void acc_steps(const TR& trd, const char G4_LDS* t,
+                                          const bf16x8 (&b)[2], f32x16 (&acc)[NB]) {
+  static_assert(kAhead == 2 && NB >= 2, "prologue reads two operands");
+  bf16x8 x[kAhead];
+  x[0] = trd.template read<0, 0, 0>(t);
+  x[1] = trd.template read<0, 0, 1>(t);
+  __builtin_amdgcn_sched_barrier(0);
+  acc_pipe<NB, 0>(trd, t, b, acc, x);
+}
+
+// part += (tile rows)[32 x 16 CP ...] . frag[CP], over CP in [0, NC).
+template <int NC, int CP, class RR>
+__device__ __forceinline__ void row_pipe(const RR& rrd, const char G4_LDS* t, f32x16& part,
+                                         const bf16x8 (&frag)[NC], bf16x8 (&x)[kAhead]) {
+  if constexpr (CP < NC) {
+    part = mfma32(x[CP % kAhead], frag[CP], part);
+    if constexpr (CP + kAhead < NC) x[CP % kAhead] = rrd.template read<0, 0, CP + kAhead>(t);
+    __builtin_amdgcn_sched_barrier(0);
+    row_pipe<NC, CP + 1>(rrd, t, part, frag, x);
+  }
+}
+template <int NC, class RR>
+__device__ __forceinline__ void row_steps(const RR& rrd, const char G4_LDS* t, f32x16& part,
+                                          const bf16x8 (&frag)[NC]) {
+  static_assert(kAhead == 2 && NC >= 2, "prologue reads two operands");
+  bf16x8 x[kAhead];
+  x[0] = rrd.template read<0, 0, 0>(t);
+  x[1] = rrd.template read<0, 0, 1>(t);
+  __builtin_amdgcn_sched_barrier(0);
+  row_pipe<NC, 0>(rrd, t, part, frag, x);
+}
+
 struct RolesCfg {
   static constexpr int D = 512;
   static constexpr int kNW = 8;
@@ -175,23 +227,8 @@ struct RolesKernel {
   }
 
   // acc^T[32 d x 32 keys] += (tile^T half dh)[32 d x 32 rows] . b[32 rows x 32 keys]
-  template <int M, int B>
-  __device__ __forceinline__ void acc_step(const char G4_LDS* t, const bf16x8 (&b)[2]) {
-    if constexpr (B < C::kNB) {
-      bf16x8 x = trd.template read<16 * M, 0, B>(t);
-      acc[B] = mfma32(x, b[M], acc[B]);
-      acc_step<M, B + 1>(t, b);
-    }
-  }
-  // part[32 rows x 32 keys] = tile rows (head-dim half dh) . frag
-  template <int CP>
-  __device__ __forceinline__ void row_step(const char G4_LDS* t, f32x16& part) const {
-    if constexpr (CP < C::kNC) {
-      bf16x8 x = rrd.template read<0, 0, CP>(t);
-      part = mfma32(x, frag[CP], part);
-      row_step<CP + 1>(t, part);
-    }
-  }
+  // (acc_steps); part[32 rows x 32 keys] = tile rows (head-dim half dh) . frag
+  // (row_steps).
 
   // Rows of the accumulators: value r of a lane is query row 8 (r >> 2) +
   // 4 h32 + (r & 3); P waves finish rows r in [8 dh, 8 dh + 8).
@@ -210,8 +247,7 @@ struct RolesKernel {
     __builtin_amdgcn_sched_barrier(0);
     f32x16 sp = f32x16{};
     if (it + 1 < nsteps) issue_q(it + 1, cur ^ 1);
-    row_step<0>(qt, sp);
-    mfma_read_hint<C::kNC, 1, 1, 3>();
+    row_steps(rrd, qt, sp, frag);
     __builtin_amdgcn_sched_barrier(0);
     // the partner's rows of this partial
     const int po = 8 * (dh ^ 1);
@@ -270,9 +306,7 @@ struct RolesKernel {
         for (int e = 0; e < 4; ++e) pb[m][4 * q4 + e] = (__bf16)v[e];
       }
     __builtin_amdgcn_sched_barrier(0);
-    acc_step<0, 0>(dot, pb);
-    acc_step<1, 0>(dot, pb);
-    mfma_read_hint<2 * C::kNB, 1, 2, 6>();
+    acc_steps(trd, dot, pb, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -287,8 +321,7 @@ struct RolesKernel {
 
     __builtin_amdgcn_sched_barrier(0);
     f32x16 dp = f32x16{};
-    row_step<0>(dot, dp);
-    mfma_read_hint<C::kNC, 1, 1, 3>();
+    row_steps(rrd, dot, dp, frag);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4)
@@ -336,9 +369,7 @@ struct RolesKernel {
       *(G4_GLOBAL bf16x4*)(tile + ds_lane + 16) = bf16x4{x[4], x[5], x[6], x[7]};
     }
     __builtin_amdgcn_sched_barrier(0);
-    acc_step<0, 0>(qt, db);
-    acc_step<1, 0>(qt, db);
-    mfma_read_hint<2 * C::kNB, 1, 2, 6>();
+    acc_steps(trd, qt, db, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -602,22 +633,6 @@ struct Roles256Kernel {
       }
     }
   }
-  template <int M, int B>
-  __device__ __forceinline__ void acc_step(const char G4_LDS* t, const bf16x8 (&b)[2]) {
-    if constexpr (B < C::kNB) {
-      bf16x8 x = trd.template read<16 * M, 0, B>(t);
-      acc[B] = mfma32(x, b[M], acc[B]);
-      acc_step<M, B + 1>(t, b);
-    }
-  }
-  template <int CP>
-  __device__ __forceinline__ void row_step(const char G4_LDS* t, f32x16& part) const {
-    if constexpr (CP < C::kNC) {
-      bf16x8 x = rrd.template read<0, 0, CP>(t);
-      part = mfma32(x, frag[CP], part);
-      row_step<CP + 1>(t, part);
-    }
-  }
   __device__ __forceinline__ char G4_LDS* pslot(int q4) const {
     return smem + C::kLdsP + ((kb * 4 + q4) * 64 + lane) * 16;
   }
@@ -633,8 +648,7 @@ struct Roles256Kernel {
     __builtin_amdgcn_sched_barrier(0);
     f32x16 sv = f32x16{};
     if (it + 1 < nsteps) issue_q(it + 1, cur ^ 1);
-    row_step<0>(qt, sv);
-    mfma_read_hint<C::kNC, 1, 1, 3>();
+    row_steps(rrd, qt, sv, frag);
     __builtin_amdgcn_sched_barrier(0);
 
     const float* ld = (const float*)(smem + C::kLdsLd + cur * 256);
@@ -674,9 +688,7 @@ struct Roles256Kernel {
     barrier_lds();  // B2
 
     __builtin_amdgcn_sched_barrier(0);
-    acc_step<0, 0>(dot, pb);
-    acc_step<1, 0>(dot, pb);
-    mfma_read_hint<2 * C::kNB, 1, 2, 6>();
+    acc_steps(trd, dot, pb, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -687,8 +699,7 @@ struct Roles256Kernel {
     const char G4_LDS* dot = smem + C::kLdsDo + cur * C::kTile;
     __builtin_amdgcn_sched_barrier(0);
     f32x16 dp = f32x16{};
-    row_step<0>(dot, dp);
-    mfma_read_hint<C::kNC, 1, 1, 3>();
+    row_steps(rrd, dot, dp, frag);
     __builtin_amdgcn_sched_barrier(0);
     if (it + 1 < nsteps) issue_do(it + 1, cur ^ 1);
     barrier_lds();  // B2
@@ -724,9 +735,7 @@ struct Roles256Kernel {
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    acc_step<0, 0>(qt, db);
-    acc_step<1, 0>(qt, db);
-    mfma_read_hint<2 * C::kNB, 1, 2, 6>();
+    acc_steps(trd, qt, db, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
 
