@@ -86,58 +86,6 @@ __device__ __forceinline__ bool dq_row_key_ends(const BwdParams& a, const Seq& s
   return need;
 }
 
-// The two MFMA products of the role kernels with kAhead LDS operand reads in
-// flight: read n + kAhead is issued right after MFMA n and sched_barrier pins
-// that order.  Left to itself the scheduler falls back to one read per MFMA,
-// each waited for, at the register budget of two waves per SIMD.
-constexpr int kAhead = 2;
-
-// acc[B] += (tile^T rows 16 M ...)[32 x 16] . b[M], over M in {0, 1}, B in [0, NB).
-template <int NB, int N, class TR>
-__device__ __forceinline__ void acc_pipe(const TR& trd, const char G4_LDS* t,
-                                         const bf16x8 (&b)[2], f32x16 (&acc)[NB],
-                                         bf16x8 (&x)[kAhead]) {
-  if constexpr (N < 2 * NB) {
-    acc[N % NB] = mfma32(x[N % kAhead], b[N / NB], acc[N % NB]);
-    if constexpr (N + kAhead < 2 * NB)
-      x[N % kAhead] = trd.template read<16 * ((N + kAhead) / NB), 0, (N + kAhead) % NB>(t);
-    __builtin_amdgcn_sched_barrier(0);
-    acc_pipe<NB, N + 1>(trd, t, b, acc, x);
-  }
-}
-template <int NB, class TR>
-__device__ __forceinline__ void acc_steps(const TR& trd, const char G4_LDS* t,
-                                          const bf16x8 (&b)[2], f32x16 (&acc)[NB]) {
-  static_assert(kAhead == 2 && NB >= 2, "prologue reads two operands");
-  bf16x8 x[kAhead];
-  x[0] = trd.template read<0, 0, 0>(t);
-  x[1] = trd.template read<0, 0, 1>(t);
-  __builtin_amdgcn_sched_barrier(0);
-  acc_pipe<NB, 0>(trd, t, b, acc, x);
-}
-
-// part += (tile rows)[32 x 16 CP ...] . frag[CP], over CP in [0, NC).
-template <int NC, int CP, class RR>
-__device__ __forceinline__ void row_pipe(const RR& rrd, const char G4_LDS* t, f32x16& part,
-                                         const bf16x8 (&frag)[NC], bf16x8 (&x)[kAhead]) {
-  if constexpr (CP < NC) {
-    part = mfma32(x[CP % kAhead], frag[CP], part);
-    if constexpr (CP + kAhead < NC) x[CP % kAhead] = rrd.template read<0, 0, CP + kAhead>(t);
-    __builtin_amdgcn_sched_barrier(0);
-    row_pipe<NC, CP + 1>(rrd, t, part, frag, x);
-  }
-}
-template <int NC, class RR>
-__device__ __forceinline__ void row_steps(const RR& rrd, const char G4_LDS* t, f32x16& part,
-                                          const bf16x8 (&frag)[NC]) {
-  static_assert(kAhead == 2 && NC >= 2, "prologue reads two operands");
-  bf16x8 x[kAhead];
-  x[0] = rrd.template read<0, 0, 0>(t);
-  x[1] = rrd.template read<0, 0, 1>(t);
-  __builtin_amdgcn_sched_barrier(0);
-  row_pipe<NC, 0>(rrd, t, part, frag, x);
-}
-
 struct RolesCfg {
   static constexpr int D = 512;
   static constexpr int kNW = 8;

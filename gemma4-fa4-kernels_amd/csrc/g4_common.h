@@ -463,4 +463,73 @@ struct WorkQueue {
   }
 };
 
+// MFMA chains with A LDS operand reads in flight (kAhead unless a caller
+// picks another depth): read n + A is issued right after MFMA n and
+// sched_barrier pins that order.  Left to itself the scheduler falls back to
+// one read per MFMA, each waited for, whenever registers are tight.
+constexpr int kAhead = 2;
+
+// acc[B] += (tile^T rows 16 M ...)[32 x 16] . b[M], over M in {0, 1}, B in [0, NB).
+template <int NB, int N, class TR>
+__device__ __forceinline__ bf16x8 acc_read(const TR& trd, const char G4_LDS* t) {
+  return trd.template read<16 * (N / NB), 0, N % NB>(t);
+}
+template <int NB, int A, int N, class TR>
+__device__ __forceinline__ void acc_pipe(const TR& trd, const char G4_LDS* t,
+                                         const bf16x8 (&b)[2], f32x16 (&acc)[NB],
+                                         bf16x8 (&x)[A]) {
+  if constexpr (N < 2 * NB) {
+    acc[N % NB] = mfma32(x[N % A], b[N / NB], acc[N % NB]);
+    if constexpr (N + A < 2 * NB) x[N % A] = acc_read<NB, N + A>(trd, t);
+    __builtin_amdgcn_sched_barrier(0);
+    acc_pipe<NB, A, N + 1>(trd, t, b, acc, x);
+  }
+}
+template <int NB, int A, int N, class TR>
+__device__ __forceinline__ void acc_prologue(const TR& trd, const char G4_LDS* t,
+                                             bf16x8 (&x)[A]) {
+  if constexpr (N < A) {
+    x[N] = acc_read<NB, N>(trd, t);
+    acc_prologue<NB, A, N + 1>(trd, t, x);
+  }
+}
+template <int NB, int A = kAhead, class TR>
+__device__ __forceinline__ void acc_steps(const TR& trd, const char G4_LDS* t,
+                                          const bf16x8 (&b)[2], f32x16 (&acc)[NB]) {
+  static_assert(A >= 1 && A <= 2 * NB, "read depth");
+  bf16x8 x[A];
+  acc_prologue<NB, A, 0>(trd, t, x);
+  __builtin_amdgcn_sched_barrier(0);
+  acc_pipe<NB, A, 0>(trd, t, b, acc, x);
+}
+
+// part += (tile rows)[32 x 16 CP ...] . frag[CP], over CP in [0, NC).
+template <int NC, int A, int CP, class RR>
+__device__ __forceinline__ void row_pipe(const RR& rrd, const char G4_LDS* t, f32x16& part,
+                                         const bf16x8 (&frag)[NC], bf16x8 (&x)[A]) {
+  if constexpr (CP < NC) {
+    part = mfma32(x[CP % A], frag[CP], part);
+    if constexpr (CP + A < NC) x[CP % A] = rrd.template read<0, 0, CP + A>(t);
+    __builtin_amdgcn_sched_barrier(0);
+    row_pipe<NC, A, CP + 1>(rrd, t, part, frag, x);
+  }
+}
+template <int A, int N, class RR>
+__device__ __forceinline__ void row_prologue(const RR& rrd, const char G4_LDS* t,
+                                             bf16x8 (&x)[A]) {
+  if constexpr (N < A) {
+    x[N] = rrd.template read<0, 0, N>(t);
+    row_prologue<A, N + 1>(rrd, t, x);
+  }
+}
+template <int NC, int A = kAhead, class RR>
+__device__ __forceinline__ void row_steps(const RR& rrd, const char G4_LDS* t, f32x16& part,
+                                          const bf16x8 (&frag)[NC]) {
+  static_assert(A >= 1 && A <= NC, "read depth");
+  bf16x8 x[A];
+  row_prologue<A, 0>(rrd, t, x);
+  __builtin_amdgcn_sched_barrier(0);
+  row_pipe<NC, A, 0>(rrd, t, part, frag, x);
+}
+
 }  // namespace g4

@@ -463,26 +463,16 @@ struct WideCfg {
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 };
 
-// Interleave a region of N MFMAs with DS reads, VALU work and VMEM issues.
-template <int N, int DS_PRE, int DS_PER, int VALU_PER, int VMEM_EVERY>
-__device__ __forceinline__ void region_hint() {
-  __builtin_amdgcn_sched_group_barrier(0x100, DS_PRE, 0);
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, DS_PER, 0);
-    if constexpr (VALU_PER > 0) __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER, 0);
-    if constexpr (VMEM_EVERY > 0)
-      if (i % VMEM_EVERY == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-  }
-}
-
 template <int D>
 struct FwdWide {
   using C = WideCfg<D>;
   static constexpr int kNC = C::kNC;
   static constexpr int kNB = C::kNB;
   static constexpr int BN = C::kBN;
+  // Operand reads in flight in the S and P.V chains: one wave per SIMD has no
+  // other wave to cover LDS latency (2.79 ms on config 2 with the scheduler's
+  // one read per MFMA, 2.66 with two in flight, 2.56-2.59 with three or four).
+  static constexpr int kAhead = 4;
 
   char G4_LDS* smem;
   Seq sq;
@@ -512,24 +502,6 @@ struct FwdWide {
       vcp.issue(vbase + row0 * vstride, dst);
     else
       vcp.issue_clamped(vbase + row0 * vstride, vstride, sq.lk - row0, dst);
-  }
-
-  template <int CP>
-  __device__ __forceinline__ void s_mma(const char G4_LDS* kt, f32x16& acc) const {
-    if constexpr (CP < kNC) {
-      bf16x8 kfrag = krd.template read<0, 0, CP>(kt);
-      acc = mfma32(kfrag, qf[CP], acc);
-      s_mma<CP + 1>(kt, acc);
-    }
-  }
-
-  template <int HK, int B>
-  __device__ __forceinline__ void pv_mma(const char G4_LDS* vt, const bf16x8& pb) {
-    if constexpr (B < kNB) {
-      bf16x8 vfrag = vrd.template read<16 * HK, 0, B>(vt);
-      o_acc[B] = mfma32(vfrag, pb, o_acc[B]);
-      pv_mma<HK, B + 1>(vt, pb);
-    }
   }
 
   // Softmax of one tile's raw scores (keys kb0 + ...) into bf16 P.
@@ -645,8 +617,7 @@ __global__ void __launch_bounds__(256, 1) fwd_wide_kernel(FwdParams a) {
     }
     barrier_lds();
     __builtin_amdgcn_sched_barrier(0);
-    ker.template s_mma<0>(ker.smem + C::kLdsK, s_cur);
-    mfma_pipeline_hint<K::kNC, 3, 1>();
+    row_steps<K::kNC, K::kAhead>(ker.krd, ker.smem + C::kLdsK, s_cur, ker.qf);
     __builtin_amdgcn_sched_barrier(0);
   }
   for (int it = 0; it < ntiles; ++it) {
@@ -664,9 +635,9 @@ __global__ void __launch_bounds__(256, 1) fwd_wide_kernel(FwdParams a) {
     f32x16 s_nxt = {};
     bf16x8 pb[2];
     if (it + 1 < ntiles) {
-      ker.template s_mma<0>(ker.smem + C::kLdsK + nxt * C::kTile, s_nxt);
+      row_steps<K::kNC, K::kAhead>(ker.krd, ker.smem + C::kLdsK + nxt * C::kTile, s_nxt,
+                                   ker.qf);
       ker.softmax(s_cur, kb0, pb);
-      region_hint<K::kNC, 3, 1, 4, 2>();
     } else {
       ker.softmax(s_cur, kb0, pb);
     }
@@ -674,9 +645,7 @@ __global__ void __launch_bounds__(256, 1) fwd_wide_kernel(FwdParams a) {
 
     // ---- region B: O^T += V(it)^T P(it)^T
     const char G4_LDS* vt = ker.smem + C::kLdsV + cur * C::kTile;
-    ker.template pv_mma<0, 0>(vt, pb[0]);
-    ker.template pv_mma<1, 0>(vt, pb[1]);
-    mfma_pipeline_hint<2 * K::kNB, 6, 2>();
+    acc_steps<K::kNB, K::kAhead>(ker.vrd, vt, pb, ker.o_acc);
     __builtin_amdgcn_sched_barrier(0);
     s_cur = s_nxt;
   }
