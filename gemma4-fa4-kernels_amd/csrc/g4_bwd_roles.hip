@@ -894,22 +894,6 @@ struct DqRolesKernel {
     return smem + C::kLdsX + ((sl * 4 + q4) * 64 + lane) * 16;
   }
 
-  template <int CP>
-  __device__ __forceinline__ void part_step(const char G4_LDS* t, f32x16& part) const {
-    if constexpr (CP < C::kNC) {
-      bf16x8 x = rrd.template read<0, 0, CP>(t);
-      part = mfma32(x, frag[CP], part);
-      part_step<CP + 1>(t, part);
-    }
-  }
-  template <int HK, int B>
-  __device__ __forceinline__ void dq_step(const char G4_LDS* kt, const bf16x8& ds) {
-    if constexpr (B < C::kNB) {
-      bf16x8 x = trd.template read<16 * HK, 0, B>(kt);
-      acc[B] = mfma32(x, ds, acc[B]);
-      dq_step<HK, B + 1>(kt, ds);
-    }
-  }
 
   __device__ __forceinline__ void step(int cur, int it, int ntiles, int t_first) {
     const int kb0 = (t_first + it) * C::kBN;
@@ -921,8 +905,7 @@ struct DqRolesKernel {
     __builtin_amdgcn_sched_barrier(0);
     f32x16 part = f32x16{};
     if (it + 1 < ntiles) issue_k(kb0 + C::kBN, cur ^ 1);
-    part_step<0>(role == 0 ? kt : vt, part);
-    mfma_read_hint<C::kNC, 1, 1, 3>();
+    row_steps(rrd, role == 0 ? kt : vt, part, frag);
     __builtin_amdgcn_sched_barrier(0);
     const int own = 4 * qg + 2 * role + dh;
 #pragma unroll
@@ -993,9 +976,7 @@ struct DqRolesKernel {
     }
 
     __builtin_amdgcn_sched_barrier(0);
-    dq_step<0, 0>(kt, dsb[0]);
-    dq_step<1, 0>(kt, dsb[1]);
-    mfma_read_hint<2 * C::kNB, 1, 2, 4>();
+    acc_steps(trd, kt, dsb, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
 };
@@ -1179,22 +1160,6 @@ struct DqRoles256Kernel {
   __device__ __forceinline__ char G4_LDS* xslot(int sl, int q4) const {
     return smem + C::kLdsX + ((sl * 4 + q4) * 64 + lane) * 16;
   }
-  template <int CP>
-  __device__ __forceinline__ void part_step(const char G4_LDS* t, f32x16& part) const {
-    if constexpr (CP < C::kNC) {
-      bf16x8 x = rrd.template read<0, 0, CP>(t);
-      part = mfma32(x, frag[CP], part);
-      part_step<CP + 1>(t, part);
-    }
-  }
-  template <int HK, int B>
-  __device__ __forceinline__ void dq_step(const char G4_LDS* kt, const bf16x8& ds) {
-    if constexpr (B < C::kNB) {
-      bf16x8 x = trd.template read<16 * HK, 0, B>(kt);
-      acc[B] = mfma32(x, ds, acc[B]);
-      dq_step<HK, B + 1>(kt, ds);
-    }
-  }
 
   // Rows of the tiles are keys 8 (r >> 2) + 4 h32 + (r & 3); lanes own queries.
   __device__ __forceinline__ void step(int cur, int it, int ntiles, int t_first) {
@@ -1207,8 +1172,7 @@ struct DqRoles256Kernel {
     __builtin_amdgcn_sched_barrier(0);
     f32x16 part = f32x16{};
     if (it + 1 < ntiles) issue_k(kb0 + C::kBN, cur ^ 1);
-    part_step<0>(role == 0 ? kt : vt, part);
-    mfma_read_hint<C::kNC, 1, 1, 3>();
+    row_steps(rrd, role == 0 ? kt : vt, part, frag);
     __builtin_amdgcn_sched_barrier(0);
 
     if (role == 0) {
@@ -1264,9 +1228,7 @@ struct DqRoles256Kernel {
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    dq_step<0, 0>(kt, dsb[0]);
-    dq_step<1, 0>(kt, dsb[1]);
-    mfma_read_hint<2 * C::kNB, 1, 2, 4>();
+    acc_steps(trd, kt, dsb, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
 };

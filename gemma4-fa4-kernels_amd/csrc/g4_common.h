@@ -273,19 +273,6 @@ __device__ __forceinline__ void mfma_pipeline_hint() {
   }
 }
 
-// Scheduling hint for NR operand reads of DPR DS instructions each, every
-// read feeding MPR MFMAs: PRE DS instructions first, then (MPR MFMAs, DPR DS
-// instructions) repeated.  Region delimited by sched_barrier(0).
-template <int NR, int MPR, int DPR, int PRE>
-__device__ __forceinline__ void mfma_read_hint() {
-  __builtin_amdgcn_sched_group_barrier(0x100, PRE, 0);
-#pragma unroll
-  for (int i = 0; i < NR; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, MPR, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, DPR, 0);
-  }
-}
-
 // Sequence geometry resolved from a problem (fixed or packed).
 struct Seq {
   int lq, lk;          // lengths
