@@ -26,6 +26,13 @@ struct FwdParams {
   int doc_pass;
 };
 
+// Query (0..31, within its 32-query row) at position p of a dS tile's key row:
+// accumulator value r of lane half h sits at p = 16 h + r and holds query
+// 8 (r >> 2) + 4 h + (r & 3).
+__host__ __device__ inline int ds_query_at(int p) {
+  return 8 * ((p & 15) >> 2) + 4 * (p >> 4) + (p & 3);
+}
+
 struct BwdParams {
   g4_problem p;
   const __bf16* q;
@@ -50,7 +57,9 @@ struct BwdParams {
   // key tile c, row r) at ((h * ds_cols + c) * ds_rows + r) * 4 KB.  Head dim
   // 256 (band): tile (h, r, key tile c) at ((h * ds_rows + r) * ds_cols +
   // c - ds_band_first(r)) * 4 KB for c - ds_band_first(r) < ds_cols.  Each tile
-  // is [64 keys][32 queries] bf16.
+  // is [64 keys][32 positions] bf16: position p holds query p of the row in the
+  // dense layout and query ds_query_at(p) in the band (the MFMA accumulator
+  // order, so each lane stores one 32-byte run).
   __bf16* ds;
   int ds_rows, ds_cols;
   // Head dim 256 dQ after the stored-dS pass: only the query tiles whose vision
