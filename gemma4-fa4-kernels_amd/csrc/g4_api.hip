@@ -121,10 +121,15 @@ size_t delta_bytes(const g4_problem& p) {
 //   at the tile of the row's first query's window start: (W + 30) / 64 + 2
 //   tiles cover every key the row's window and causal part admit, and with
 //   bidirectional vision up to 18 more (1152 keys) hold keys of vision spans
-//   that reach past the row's causal end, as far as the 16 GiB cap allows.
+//   that reach past the row's causal end, as far as the budget allows.
 //   The dQ stage recomputes the query tiles whose spans reach past the band.
-// Used while the buffer stays within 16 GiB.
+// Used while the buffer stays within the problem's ds_budget (0: 16 GiB,
+// negative: no stored tiles); otherwise the dQ stage recomputes S and dP.
 constexpr size_t kDsCap = size_t(16) << 30;
+size_t ds_cap(const g4_problem& p) {
+  if (p.ds_budget < 0) return 0;
+  return p.ds_budget == 0 ? kDsCap : (size_t)p.ds_budget;
+}
 void ds_geometry(const g4_problem& p, int* rows, int* cols) {
   const int64_t r = p.cu_seqlens_q ? p.total_q / 32 + p.num_seqs
                                    : (int64_t)p.num_seqs * ((p.seqlen_q + 31) / 32);
@@ -133,7 +138,7 @@ void ds_geometry(const g4_problem& p, int* rows, int* cols) {
     const int base = (p.window + 30) / 64 + 2;
     const bool vis = p.vision_ids != nullptr && p.bidirectional_vision;
     const int64_t per_col = r * p.num_q_heads * 4096;
-    const int64_t fit = per_col > 0 ? (int64_t)kDsCap / per_col : base;
+    const int64_t fit = per_col > 0 ? (int64_t)(ds_cap(p) / (size_t)per_col) : base;
     *cols = (int)std::max<int64_t>(base, std::min<int64_t>(base + (vis ? 18 : 0), fit));
   } else {
     *cols = (p.seqlen_k + 63) / 64;
@@ -147,7 +152,7 @@ size_t ds_bytes(const g4_problem& p) {
   int rows, cols;
   ds_geometry(p, &rows, &cols);
   const size_t b = (size_t)rows * cols * p.num_q_heads * 4096;
-  return b <= kDsCap ? b : 0;
+  return b <= ds_cap(p) ? b : 0;
 }
 // One int per (sequence, 32-query group, query head) for the head-dim 512
 // forward's second pass.
@@ -164,6 +169,7 @@ int g4_abi_version(void) { return G4_ABI_VERSION; }
 const char* g4_last_error(void) { return g_last_error.c_str(); }
 
 size_t g4_workspace_bytes(const g4_problem* p, int phase) {
+  g_last_error.clear();
   if (check_problem(p) != G4_OK) return 0;
   size_t b = align256(g4::spans_bytes(*p)) + g4::raise_flags_bytes(*p);
   if (phase == 1) b += g4::delta_bytes(*p) + g4::ds_bytes(*p) + g4::kSchedBytes;
@@ -173,6 +179,7 @@ size_t g4_workspace_bytes(const g4_problem* p, int phase) {
 int g4_attn_fwd(const g4_problem* p, const void* q, g4_layout ql, const void* k, g4_layout kl,
                 const void* v, g4_layout vl, void* o, g4_layout ol, float* lse, void* ws,
                 size_t ws_bytes, void* stream) {
+  g_last_error.clear();
   G4_TRY(check_problem(p));
   G4_TRY(check_operand(q, ql, "q"));
   G4_TRY(check_operand(k, kl, "k"));
@@ -224,6 +231,7 @@ static int fill_bwd(g4::BwdParams& a, const g4_problem* p, const void* q, g4_lay
 
 int g4_attn_bwd_delta(const g4_problem* p, const void* o, g4_layout ol, const void* dout,
                       g4_layout dol, const float* dlse, void* ws, size_t ws_bytes, void* stream) {
+  g_last_error.clear();
   G4_TRY(check_problem(p));
   G4_TRY(check_operand(o, ol, "o"));
   G4_TRY(check_operand(dout, dol, "dout"));
@@ -252,6 +260,7 @@ int g4_attn_bwd_dkdv(const g4_problem* p, const void* q, g4_layout ql, const voi
                      g4_layout kl, const void* v, g4_layout vl, const void* dout, g4_layout dol,
                      const float* lse, void* dk, g4_layout dkl, void* dv, g4_layout dvl, void* ws,
                      size_t ws_bytes, void* stream) {
+  g_last_error.clear();
   G4_TRY(check_problem(p));
   G4_TRY(check_operand(q, ql, "q"));
   G4_TRY(check_operand(k, kl, "k"));
@@ -278,6 +287,7 @@ int g4_attn_bwd_dkdv(const g4_problem* p, const void* q, g4_layout ql, const voi
 int g4_attn_bwd_dq(const g4_problem* p, const void* q, g4_layout ql, const void* k, g4_layout kl,
                    const void* v, g4_layout vl, const void* dout, g4_layout dol, const float* lse,
                    void* dq, g4_layout dql, void* ws, size_t ws_bytes, void* stream) {
+  g_last_error.clear();
   G4_TRY(check_problem(p));
   G4_TRY(check_operand(q, ql, "q"));
   G4_TRY(check_operand(k, kl, "k"));
@@ -312,6 +322,7 @@ int g4_attn_bwd(const g4_problem* p, const void* q, g4_layout ql, const void* k,
 
 int g4_mask_materialize(const g4_problem* p, uint8_t* out, void* ws, size_t ws_bytes,
                         void* stream) {
+  g_last_error.clear();
   G4_TRY(check_problem(p));
   if (out == nullptr) return fail(G4_ERR_INVALID, "out is NULL");
   (void)ws;
@@ -323,6 +334,7 @@ int g4_mask_materialize(const g4_problem* p, uint8_t* out, void* ws, size_t ws_b
 
 int g4_tile_ranges(const g4_problem* p, int direction, int row_tile, int32_t* out, void* ws,
                    size_t ws_bytes, void* stream) {
+  g_last_error.clear();
   G4_TRY(check_problem(p));
   if (out == nullptr) return fail(G4_ERR_INVALID, "out is NULL");
   if (direction != 0 && direction != 1) return fail(G4_ERR_INVALID, "direction must be 0 or 1");

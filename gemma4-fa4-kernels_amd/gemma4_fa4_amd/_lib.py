@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be imported before the HIP library is loaded)
 from .errors import UnsupportedMI355XPath
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libgemma4_attn.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 G4_OK = 0
 G4_ERR_INVALID = 1
@@ -65,6 +65,7 @@ class G4Problem(ctypes.Structure):
         ("document_ids", ctypes.c_void_p),
         ("lse_batch_stride", ctypes.c_int64),
         ("lse_head_stride", ctypes.c_int64),
+        ("ds_budget", ctypes.c_int64),
     ]
 
 

@@ -402,6 +402,21 @@ def _layout(t: torch.Tensor, packed: bool) -> G4Layout:
     return G4Layout(t.stride(0), t.stride(1), t.stride(2))
 
 
+def _meets_operand_contract(t: torch.Tensor) -> bool:
+    """Whether the library accepts ``t`` as a bf16 operand as it stands.
+
+    Unit head-dim stride, positive outer strides that are multiples of 8
+    elements (token stride below 2^24), and a 16-byte aligned base.
+    """
+    strides = t.stride()
+    return (
+        strides[-1] == 1
+        and all(s > 0 and s % 8 == 0 for s in strides[:-1])
+        and strides[-3] < (1 << 24)
+        and t.data_ptr() % 16 == 0
+    )
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -425,6 +440,9 @@ class _Plan:
     cu_k: torch.Tensor | None = None
     vision: torch.Tensor | None = None
     documents: torch.Tensor | None = None
+    # Bytes of the backward workspace for stored dS tiles (0: library default,
+    # negative: none, so the dQ stage recomputes S and dP).
+    ds_budget: int = 0
     # Cumulative-array checks still to run before the first launch.
     pending: _CumulativeCheck | None = field(default=None, repr=False, compare=False)
 
@@ -455,6 +473,7 @@ class _Plan:
         else:
             p.lse_batch_stride = self.num_q_heads * self.seqlen_q
             p.lse_head_stride = self.seqlen_q
+        p.ds_budget = self.ds_budget
         return p
 
     def lse_shape(self) -> tuple[int, ...]:
@@ -500,7 +519,8 @@ class _Plan:
 
     def backward(self, q, k, v, out, dout, lse, dlse):
         lib = _lib.load()
-        if dout.stride(-1) != 1 or any(s % 8 for s in dout.stride()[:-1]):
+        if not _meets_operand_contract(dout):
+            # e.g. a broadcast gradient of a sum, or a view off 16-byte alignment
             dout = dout.contiguous()
         if dlse is not None:
             dlse = dlse.to(torch.float32).contiguous()

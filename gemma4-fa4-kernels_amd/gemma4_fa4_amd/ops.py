@@ -31,6 +31,7 @@ def make_plan(
     cu_k: torch.Tensor | None = None,
     total_q: int | None = None,
     total_k: int | None = None,
+    ds_budget: int = 0,
 ) -> _Plan:
     packed = cu_q is not None
     return _Plan(
@@ -49,6 +50,7 @@ def make_plan(
         cu_k=cu_k,
         vision=None if vision is None else vision.to(torch.int32).contiguous(),
         documents=None if documents is None else documents.to(torch.int32).contiguous(),
+        ds_budget=ds_budget,
     )
 
 

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define G4_ABI_VERSION 1
+#define G4_ABI_VERSION 2
 
 enum g4_status {
   G4_OK = 0,
@@ -72,6 +72,14 @@ typedef struct g4_problem {
   const int32_t* document_ids; /* device, NULL when absent */
   int64_t lse_batch_stride;    /* fixed mode only */
   int64_t lse_head_stride;
+  /* Bytes of the backward workspace that may hold dS tiles stored by the
+   * dK/dV stage for the dQ stage: 0 = the library default (16 GiB), < 0 =
+   * none.  When the tiles a problem needs exceed the budget, none are stored
+   * and the dQ stage recomputes S and dP (slower, workspace O(T) instead of
+   * O(T * Sk)).  Results are the same either way up to fp32 summation order.
+   * The reference's global backward budget policy is the analogous knob
+   * (src/gemma4_fa4/h100.py:713-746). */
+  int64_t ds_budget;
 } g4_problem;
 
 /* Library ABI version (G4_ABI_VERSION). */

@@ -46,6 +46,67 @@ def test_workspace_query_and_invalid_problem_are_reported():
         _lib.check(_lib.G4_ERR_UNSUPPORTED)
 
 
+def test_an_earlier_rejection_does_not_fail_a_later_valid_problem():
+    # g4_last_error is per call: a rejected problem on this thread must not make
+    # a later valid problem whose workspace is legitimately 0 bytes look failed.
+    import ctypes
+    lib = _lib.load()
+    bad = _lib.G4Problem(num_seqs=1, seqlen_q=128, seqlen_k=128, num_q_heads=32,
+                         num_kv_heads=16, head_dim=128)
+    assert lib.g4_workspace_bytes(ctypes.byref(bad), 0) == 0
+    assert lib.g4_last_error()
+    good = _lib.G4Problem(num_seqs=1, seqlen_q=128, seqlen_k=128, num_q_heads=32,
+                          num_kv_heads=16, head_dim=256, window=1024)
+    assert lib.g4_workspace_bytes(ctypes.byref(good), 0) == 0
+    assert lib.g4_last_error() == b""
+    plan = att._Plan(packed=False, num_seqs=1, seqlen_q=128, seqlen_k=128, num_q_heads=32,
+                     num_kv_heads=16, head_dim=256, window=1024, bidirectional=False,
+                     total_q=128, total_k=128)
+    lib.g4_workspace_bytes(ctypes.byref(bad), 1)
+    assert plan.workspace_bytes(0) == 0  # does not raise
+
+
+def _ws(**kw):
+    import ctypes
+    p = _lib.G4Problem(num_seqs=1, num_q_heads=32, **kw)
+    return _lib.load().g4_workspace_bytes(ctypes.byref(p), 1)
+
+
+def test_ds_budget_sizes_the_stored_dS_tiles():
+    # head dim 512 causal, S=4096: 128 rows x 64 key tiles x 32 heads x 4 KB
+    d512 = dict(seqlen_q=4096, seqlen_k=4096, num_kv_heads=4, head_dim=512, window=0)
+    dense = 128 * 64 * 32 * 4096
+    assert _ws(**d512) - _ws(**d512, ds_budget=-1) == dense
+    assert _ws(**d512, ds_budget=dense) - _ws(**d512, ds_budget=-1) == dense
+    assert _ws(**d512, ds_budget=dense - 1) == _ws(**d512, ds_budget=-1)
+    # head dim 256 window 1024: a band of (1024 + 30) // 64 + 2 = 18 key tiles per row
+    d256 = dict(seqlen_q=4096, seqlen_k=4096, num_kv_heads=16, head_dim=256, window=1024)
+    band = 128 * 18 * 32 * 4096
+    assert _ws(**d256) - _ws(**d256, ds_budget=-1) == band
+    assert _ws(**d256, ds_budget=band - 1) == _ws(**d256, ds_budget=-1)
+    # the default budget is 16 GiB: exactly a 16384-token global sequence's tiles;
+    # one more 32-query row and none are stored
+    at = dict(seqlen_q=16384, seqlen_k=16384, num_kv_heads=4, head_dim=512, window=0)
+    assert _ws(**at) - _ws(**at, ds_budget=-1) == 16 << 30
+    big = dict(seqlen_q=16416, seqlen_k=16416, num_kv_heads=4, head_dim=512, window=0)
+    assert _ws(**big) == _ws(**big, ds_budget=-1)
+    assert _ws(**big, ds_budget=1 << 36) - _ws(**big, ds_budget=-1) == 513 * 257 * 32 * 4096
+
+
+@pytest.mark.parametrize("make,ok", [
+    (lambda: torch.zeros(1, 64, 32, 256, dtype=torch.bfloat16), True),
+    (lambda: torch.zeros(256, dtype=torch.bfloat16).expand(1, 64, 32, 256), False),
+    (lambda: torch.zeros(64, 32, 264, dtype=torch.bfloat16)[..., :256], True),
+    (lambda: torch.zeros(64 * 32 * 256 + 8, dtype=torch.bfloat16)[1:64 * 32 * 256 + 1]
+     .view(64, 32, 256), False),  # base off 16-byte alignment
+    (lambda: torch.zeros(64, 32, 260, dtype=torch.bfloat16)[..., :256], False),
+])
+def test_upstream_gradient_operand_contract(make, ok):
+    # The backward copies an upstream gradient the library would reject
+    # (broadcast, misaligned) instead of failing a valid autograd graph.
+    assert att._meets_operand_contract(make()) is ok
+
+
 def test_error_hierarchy_keeps_reference_names():
     assert issubclass(g.GlobalBackwardBudgetExceeded, g.UnsupportedH100Path)
     assert g.UnsupportedH100Path is g.UnsupportedMI355XPath
