@@ -17,7 +17,8 @@ quartiles, the same call with cold caches, the other four configurations
 packed global T=32768 backward, packed local T=131072 with vision blocks and
 documents; P counted exactly per row), per-kernel times measured with HIP
 events on the launch stream (the roofline of the dominant kernel), and the
-fp32 CPU oracle timed on a bounded sample of configuration 2 on this host.
+fp32 CPU oracle timed on this host (configuration 1 in full, forward-only and
+forward+backward of a bounded head sample of configuration 2).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        [--no-extra]
@@ -239,8 +240,27 @@ def measured_traffic(stage: str):
     return {"bytes": int(nbytes), "source": "profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"}
 
 
+def _cpu_model() -> str:
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return model
+
+
 def cpu_baseline(budget_s: float):
-    """fp32 CPU oracle (this repo's restatement of reference_attention) on a head sample of c2."""
+    """fp32 CPU oracle (this repo's restatement of reference_attention) on this host.
+
+    Configuration 1 (local d256 forward, S=2048) runs in full.  Configuration 2
+    (global d512 causal, S=8192) runs on a sample of query heads within the time
+    budget, forward-only and forward+backward; per-call times are scaled to all
+    32 heads (the heads are independent and equally costly), and the backward is
+    their difference.  `value` is configuration 2's fwd+bwd TFLOP/s.
+    """
     import torch
 
     sys.path.insert(0, ROOT)
@@ -248,36 +268,53 @@ def cpu_baseline(budget_s: float):
 
     # The GPU box grants 16 host threads per GPU whatever os.cpu_count() reports.
     torch.set_num_threads(max(1, min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", 16)))))
+    # configuration 1, every head, forward only
+    q, k, v, _do = make_inputs(torch, 1, 2048, 32, 16, 256, "cpu")
+    cu1 = [0, 2048]
+    t0 = time.perf_counter()
+    attention_fwd_bwd(q, k, v, cu1, cu1, compute_dtype=torch.float32, sliding_window=1024,
+                      q_chunk=512)
+    c1_s = time.perf_counter() - t0
+    c1_fl = flops(pairs_window(2048, 1024), 32, 256, "fwd")
+    # configuration 2, a head sample: forward, then forward + backward
     s, hq, hkv, d = 8192, 32, 4, 512
     q, k, v, do = make_inputs(torch, 1, s, hq, hkv, d, "cpu")
     cu = [0, s]
-    done = 0
-    t0 = time.perf_counter()
+    per_head = {"fwd": [], "fwd_bwd": []}
+    t_start = time.perf_counter()
     for h in range(hq):
+        t0 = time.perf_counter()
+        attention_fwd_bwd(q, k, v, cu, cu, compute_dtype=torch.float32, heads=[h], q_chunk=512)
+        t1 = time.perf_counter()
         attention_fwd_bwd(q, k, v, cu, cu, do=do, compute_dtype=torch.float32, heads=[h],
                           q_chunk=512)
-        done += 1
-        if time.perf_counter() - t0 >= budget_s:
+        t2 = time.perf_counter()
+        per_head["fwd"].append(t1 - t0)
+        per_head["fwd_bwd"].append(t2 - t1)
+        if t2 - t_start >= budget_s:
             break
-    el = time.perf_counter() - t0
-    fl = flops(pairs_causal(s), 1, d, "fwd_bwd") * done
-    model = platform.processor() or "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    done = len(per_head["fwd"])
+    fwd_ms = 1e3 * hq * statistics.mean(per_head["fwd"])
+    fb_ms = 1e3 * hq * statistics.mean(per_head["fwd_bwd"])
+    p2 = pairs_causal(s)
+    tf = lambda mode, ms: round(flops(p2, hq, d, mode) / (ms * 1e-3) / 1e12, 4)  # noqa: E731
     return {
-        "value": round(fl / el / 1e12, 4),
+        "value": tf("fwd_bwd", fb_ms),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"fp32 oracle fwd+bwd of {done}/{hq} query heads of config 2 "
-                  f"(S=8192 causal d512), {el:.1f} s; os.cpu_count()={os.cpu_count()}; {model}",
-        "seconds": round(el, 2),
+        "sample": f"fp32 oracle on this host: config 1 forward in full (S=2048, 32 heads); "
+                  f"config 2 forward and forward+backward of {done}/{hq} query heads "
+                  f"(S=8192 causal d512), {time.perf_counter() - t_start:.1f} s, scaled to 32 heads; "
+                  f"os.cpu_count()={os.cpu_count()}; {_cpu_model()}",
+        "config2_fwd_ms": round(fwd_ms, 1),
+        "config2_bwd_ms": round(fb_ms - fwd_ms, 1),
+        "config2_fwd_bwd_ms": round(fb_ms, 1),
+        "config2_fwd_tflops": tf("fwd", fwd_ms),
+        "config2_bwd_tflops": tf("bwd", fb_ms - fwd_ms),
+        "config1_fwd_ms": round(1e3 * c1_s, 1),
+        "config1_fwd_tflops": round(c1_fl / c1_s / 1e12, 4),
+        "os_cpu_count": os.cpu_count(),
     }
 
 
@@ -290,6 +327,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-extra", action="store_true",
                     help="only configuration 2 (skip configurations 1, 3, 4, 5 and the cold-cache run)")
+    ap.add_argument("--extra-configs", default="1,3,4,5",
+                    help="comma-separated configurations timed besides configuration 2")
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): this build "
@@ -311,14 +351,16 @@ def main() -> int:
                                                                 reps=max(3, args.steps))
     extra = {}
     if not args.no_extra:
-        # Cold caches: a 1 GiB write (4x the 256 MB Infinity Cache) before each call.
-        junk = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-        cold, _ = run_workload(torch, g, wl.config2(), steps=max(3, args.steps // 2),
-                               warmup=1, dev=dev, flush=lambda: junk.fill_(1))
-        head["fwd_bwd_cold_ms"] = cold["fwd_bwd_ms"]
-        head["fwd_bwd_cold_tflops"] = cold["fwd_bwd_tflops"]
-        del junk
-        for cfg in (wl.config1, wl.config3, wl.config4, wl.config5):
+        if not args.no_cold:
+            # Cold caches: a 1 GiB write (4x the 256 MB Infinity Cache) before each call.
+            junk = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+            cold, _ = run_workload(torch, g, wl.config2(), steps=max(3, args.steps // 2),
+                                   warmup=1, dev=dev, flush=lambda: junk.fill_(1))
+            head["fwd_bwd_cold_ms"] = cold["fwd_bwd_ms"]
+            head["fwd_bwd_cold_tflops"] = cold["fwd_bwd_tflops"]
+            del junk
+        chosen = [int(x) for x in args.extra_configs.split(",") if x.strip()]
+        for cfg in (getattr(wl, f"config{i}") for i in chosen if i != 2):
             w = cfg()
             extra[w.name], _ = run_workload(torch, g, w, steps=args.steps,
                                             warmup=args.warmup, dev=dev)

@@ -19,6 +19,8 @@ differentiable.  Queries are the lower-right suffix of their key sequence.
 from __future__ import annotations
 
 import ctypes
+import threading
+import weakref
 from dataclasses import dataclass, field
 
 import torch
@@ -225,14 +227,68 @@ class _CumulativeCheck:
             raise self._held
 
 
-def _cumulative_lengths(cu_q, cu_k, q, k, *, label: str):
-    # One device-to-host copy (and stream sync) for both arrays.
+class _HostValues:
+    """Host copies of small device int32 arrays, reused while the tensor is unchanged.
+
+    Reading ``cu_seqlens`` to the host waits for every earlier launch on the
+    stream, so a model that passes the same arrays to each of its attention
+    layers would idle the GPU between layers.  A copy is reused only for the
+    same tensor object (held weakly) at the same storage address with the same
+    version counter; every in-place torch operation on the tensor or a view of
+    it increments that counter, so such a change is always read afresh.  Writes
+    that bypass torch (a raw pointer handed to other native code) are not
+    seen; such callers pass a new tensor.
+    """
+
+    def __init__(self, capacity: int = 16):
+        self._capacity = capacity
+        self._entries: dict[int, tuple] = {}
+        self._lock = threading.Lock()
+
+    def _key(self, t: torch.Tensor):
+        return (t._version, t.data_ptr(), tuple(t.shape), t.dtype)
+
+    def lookup(self, t: torch.Tensor):
+        if t.is_inference():  # inference tensors keep no version counter
+            return None
+        with self._lock:
+            entry = self._entries.get(id(t))
+        if entry is not None and entry[0]() is t and entry[1] == self._key(t):
+            return entry[2]
+        return None
+
+    def store(self, t: torch.Tensor, values: list[int]) -> None:
+        if t.is_inference():
+            return
+        with self._lock:
+            if len(self._entries) >= self._capacity:
+                self._entries.pop(next(iter(self._entries)))
+            self._entries[id(t)] = (weakref.ref(t), self._key(t), values)
+
+
+_CU_HOST = _HostValues()
+
+
+def _host_values(cu_q: torch.Tensor, cu_k: torch.Tensor):
+    """``cu_q`` and ``cu_k`` as Python lists, with at most one device-to-host copy."""
+    q_vals = _CU_HOST.lookup(cu_q)
+    k_vals = q_vals if cu_k is cu_q else _CU_HOST.lookup(cu_k)
+    if q_vals is not None and k_vals is not None:
+        return q_vals, k_vals
     if cu_q.data_ptr() == cu_k.data_ptr() and cu_q.shape == cu_k.shape:
         q_vals = cu_q.detach().cpu().tolist()
         k_vals = q_vals
     else:
         both = torch.cat((cu_q.detach(), cu_k.detach())).cpu().tolist()
         q_vals, k_vals = both[: cu_q.numel()], both[cu_q.numel():]
+    _CU_HOST.store(cu_q, q_vals)
+    if cu_k is not cu_q:
+        _CU_HOST.store(cu_k, k_vals)
+    return q_vals, k_vals
+
+
+def _cumulative_lengths(cu_q, cu_k, q, k, *, label: str):
+    q_vals, k_vals = _host_values(cu_q, cu_k)
     if q_vals[0] != 0 or k_vals[0] != 0:
         raise ValueError(f"{label} cumulative arrays must start at zero")
     if q_vals[-1] != q.shape[0] or k_vals[-1] != k.shape[0]:

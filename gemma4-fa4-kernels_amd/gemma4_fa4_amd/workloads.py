@@ -158,14 +158,17 @@ def _runs_first_index(ids: np.ndarray) -> np.ndarray:
     return np.maximum.accumulate(idx)
 
 
-def allowed_pairs(w: Workload) -> int:
-    """Exact allowed (q, k) pairs per head, Sq = Sk per segment.
+def allowed_intervals(w: Workload) -> tuple[np.ndarray, np.ndarray]:
+    """Per token of the packed stream, the allowed keys [lo, hi] (absolute indices).
 
-    Row a (position in its segment): keys [max(first of its document run,
-    a - W + 1), a], plus, for a vision token, the later keys of its own vision
-    block (blocks are contiguous runs inside one document, by construction).
+    Sq = Sk per segment.  Row a (position in its segment) admits keys
+    [max(first of its document run, a - W + 1), a] and, for a vision token, the
+    later keys of its own vision block up to the block's end (blocks are
+    contiguous runs inside one document, by construction), so every row's
+    allowed set is one interval.
     """
-    total = 0
+    lo_all = np.empty(w.tokens, dtype=np.int64)
+    hi_all = np.empty(w.tokens, dtype=np.int64)
     start = 0
     for n in w.seg_lengths:
         a = np.arange(n, dtype=np.int64)
@@ -174,17 +177,24 @@ def allowed_pairs(w: Workload) -> int:
             lo = _runs_first_index(w.documents[start: start + n]).astype(np.int64)
         if w.window is not None:
             lo = np.maximum(lo, a - w.window + 1)
-        count = a - lo + 1
+        hi = a.copy()
         if w.vision is not None:
             vis = w.vision[start: start + n]
             key = vis.astype(np.int64)
             if w.documents is not None:
                 key = key * (1 << 20) + w.documents[start: start + n]
             last = _runs_last_index(key)
-            count = count + np.where(vis >= 0, last - a, 0)
-        total += int(count.sum())
+            hi = np.where(vis >= 0, np.maximum(a, last), a)
+        lo_all[start: start + n] = start + lo
+        hi_all[start: start + n] = start + hi
         start += n
-    return total
+    return lo_all, hi_all
+
+
+def allowed_pairs(w: Workload) -> int:
+    """Exact allowed (q, k) pairs per head (the sum of the rows' interval lengths)."""
+    lo, hi = allowed_intervals(w)
+    return int((hi - lo + 1).sum())
 
 
 def text_pairs(w: Workload) -> int:
@@ -199,14 +209,25 @@ def text_pairs(w: Workload) -> int:
     return total
 
 
-def tensors(w: Workload, device):
-    """Packed THD bf16 q, k, v, dO and int32 cu / vision / documents on `device`."""
-    g = torch.Generator().manual_seed(w.seed)
+def tensors(w: Workload, device, *, device_rng: bool = False):
+    """Packed THD bf16 q, k, v, dO and int32 cu / vision / documents on `device`.
+
+    Values are drawn on the CPU from a generator seeded with the workload's
+    seed (so every device sees the same data), or, with ``device_rng``, on
+    `device` from a device generator with the same seed (same distributions,
+    different values; seconds faster for the large configurations).
+    """
+    where = torch.device(device) if device_rng else torch.device("cpu")
+    g = torch.Generator(device=where).manual_seed(w.seed)
     t, sd = w.tokens, w.d ** -0.25
-    q = (torch.randn(t, w.hq, w.d, generator=g) * sd).to(torch.bfloat16)
-    k = (torch.randn(t, w.hkv, w.d, generator=g) * sd).to(torch.bfloat16)
-    v = torch.randn(t, w.hkv, w.d, generator=g).to(torch.bfloat16)
-    do = torch.randn(t, w.hq, w.d, generator=g).to(torch.bfloat16)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g, device=where)
+
+    q = (randn(t, w.hq, w.d) * sd).to(torch.bfloat16)
+    k = (randn(t, w.hkv, w.d) * sd).to(torch.bfloat16)
+    v = randn(t, w.hkv, w.d).to(torch.bfloat16)
+    do = randn(t, w.hq, w.d).to(torch.bfloat16)
     cu = torch.tensor(w.cu(), dtype=torch.int32)
     vis = None if w.vision is None else torch.from_numpy(w.vision)
     docs = None if w.documents is None else torch.from_numpy(w.documents)

@@ -1,0 +1,177 @@
+"""C-ABI parity of the backward without stored dS tiles (the dQ stage recomputes S and dP).
+
+The dK/dV stage stores bf16 dS tiles for the dQ stage while they fit the
+problem's ``ds_budget`` (16 GiB by default).  Past it -- a single global
+sequence longer than 16384 tokens, or packed global batches whose rows times
+longest segment pass the budget -- the dK/dV kernels run their store-less
+branch and dQ comes from the recomputing role kernels (``dq_roles_kernel``
+at head dim 512, ``dq_roles256_kernel`` at 256).  A negative budget forces
+that route at small sizes; every case is checked against the fp64 oracle with
+the reference's M1 envelopes, and against the stored-dS route.  The last test
+runs a real 16448-token global sequence through the packed adapter with the
+default budget (the route the reference's S=64K measurement takes,
+experiments/EXP-0035-h100-global-dq-d256-streaming.md:69-70).
+"""
+
+import pytest
+import torch
+
+from g4_testutil import check_forward, check_gradients, cu, qkv, vision_blocks
+from oracle.attention import attention_fwd_bwd, bf16_baseline_fwd_bwd
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _stages(q, k, v, do, dlse, cq, ck, window, *, vis=None, docs=None, ds_budget=0,
+            packed=True):
+    from gemma4_fa4_amd import ops
+
+    lq = (cq[1:] - cq[:-1])
+    lk = (ck[1:] - ck[:-1])
+    plan = ops.make_plan(
+        num_seqs=len(cq) - 1, seqlen_q=int(lq.max()), seqlen_k=int(lk.max()),
+        num_q_heads=q.shape[1], num_kv_heads=k.shape[1], head_dim=q.shape[2], window=window,
+        vision=None if vis is None else vis.to(DEV),
+        documents=None if docs is None else docs.to(DEV),
+        cu_q=cq.to(DEV) if packed else None, cu_k=ck.to(DEV) if packed else None,
+        total_q=q.shape[0], total_k=k.shape[0], ds_budget=ds_budget)
+    if not packed:  # one fixed sequence: (1, S, H, D) views of the same buffers
+        q, k, v, do = (t[None] for t in (q, k, v, do))
+        dlse = dlse[None]
+    st = ops.Stages(plan, q.to(DEV), k.to(DEV), v.to(DEV), do.to(DEV), dlse.to(DEV))
+    st.forward()
+    st.delta()
+    st.dkdv()
+    st.dq_stage()
+    torch.cuda.synchronize()
+    squeeze = (lambda t: t) if packed else (lambda t: t[0])
+    return [squeeze(t).cpu() for t in (st.o, st.lse, st.dq, st.dk, st.dv)], plan
+
+
+def _oracle(q, k, v, do, dlse, cq, ck, window, vis=None, docs=None, heads=None):
+    args = dict(sliding_window=window, vision_block_ids=None if vis is None else vis.to(DEV),
+                document_ids=None if docs is None else docs.to(DEV),
+                allow_vision_bidirectional=window is not None and vis is not None, heads=heads)
+    ref = attention_fwd_bwd(q.to(DEV), k.to(DEV), v.to(DEV), cq.tolist(), ck.tolist(),
+                            do=do.to(DEV), dlse=dlse.to(DEV), compute_dtype=torch.float64, **args)
+    _, bq, bk, bv = bf16_baseline_fwd_bwd(q.to(DEV), k.to(DEV), v.to(DEV), cq.tolist(),
+                                          ck.tolist(), do=do.to(DEV), dlse=dlse.to(DEV), **args)
+    return [t.cpu() for t in ref], [t.cpu() for t in (bq, bk, bv)]
+
+
+def _workspace_has_no_ds(plan):
+    stored = plan.workspace_bytes(1)
+    plan.ds_budget = -1
+    none = plan.workspace_bytes(1)
+    return stored == none
+
+
+@pytest.mark.parametrize("hq,hkv,packed,with_docs", [
+    (32, 4, True, False),
+    (32, 4, False, False),
+    (8, 8, True, True),
+    (16, 2, True, False),
+    (8, 1, False, False),
+])
+def test_d512_dq_recomputed_without_stored_ds(hq, hkv, packed, with_docs):
+    lq, lk = ([300, 0, 517, 96], [300, 40, 600, 96]) if packed else ([700], [700])
+    label = f"d512 recompute hq={hq} hkv={hkv} packed={packed} docs={with_docs}"
+    print(label, flush=True)
+    q, k, v, do, dlse = qkv(9100 + hq + hkv, sum(lq), sum(lk), hq, hkv, 512)
+    cq, ck = cu(lq), cu(lk)
+    docs = None
+    if with_docs:
+        docs = torch.zeros(sum(lk), dtype=torch.int32)
+        docs[sum(lk) // 3:] = 1
+    got, plan = _stages(q, k, v, do, dlse, cq, ck, None, docs=docs, ds_budget=-1, packed=packed)
+    assert _workspace_has_no_ds(plan)
+    (o_ref, l_ref, *refs), bf = _oracle(q, k, v, do, dlse, cq, ck, None, docs=docs)
+    check_forward(got[0], got[1], o_ref, l_ref, local=False, label=label)
+    check_gradients(got[2:], refs, bf, label=label)
+    if packed:  # keys of the Q-empty segment get exact-zero gradients
+        k0, k1 = lk[0], lk[0] + lk[1]
+        assert torch.all(got[3][k0:k1] == 0) and torch.all(got[4][k0:k1] == 0)
+    # the stored-dS route agrees: dK/dV to the bit (same kernel, same order),
+    # dQ to fp32 summation order
+    stored, _ = _stages(q, k, v, do, dlse, cq, ck, None, docs=docs, packed=packed)
+    assert torch.equal(stored[3], got[3]) and torch.equal(stored[4], got[4])
+    torch.testing.assert_close(stored[2].float(), got[2].float(), atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("with_vision,with_docs", [(False, False), (True, False), (True, True)])
+def test_d256_dq_recomputed_without_stored_ds(with_vision, with_docs):
+    lq, lk = [1500, 0, 900, 1300], [1500, 50, 1100, 1300]
+    label = f"d256 recompute vision={with_vision} docs={with_docs}"
+    print(label, flush=True)
+    q, k, v, do, dlse = qkv(9200 + 2 * with_vision + with_docs, sum(lq), sum(lk), 32, 16, 256)
+    cq, ck = cu(lq), cu(lk)
+    vis = vision_blocks(77, sum(lk), 5, 100, 700) if with_vision else None
+    docs = None
+    if with_docs:
+        docs = torch.zeros(sum(lk), dtype=torch.int32)
+        docs[1000:] = 1
+        docs[3000:] = 2
+    got, plan = _stages(q, k, v, do, dlse, cq, ck, 1024, vis=vis, docs=docs, ds_budget=-1)
+    assert _workspace_has_no_ds(plan)
+    (o_ref, l_ref, *refs), bf = _oracle(q, k, v, do, dlse, cq, ck, 1024, vis, docs)
+    check_forward(got[0], got[1], o_ref, l_ref, local=True, label=label)
+    check_gradients(got[2:], refs, bf, label=label)
+    stored, _ = _stages(q, k, v, do, dlse, cq, ck, 1024, vis=vis, docs=docs)
+    assert torch.equal(stored[3], got[3]) and torch.equal(stored[4], got[4])
+    torch.testing.assert_close(stored[2].float(), got[2].float(), atol=2e-2, rtol=1e-2)
+
+
+def test_d256_budget_between_the_band_and_its_vision_extension():
+    # A budget that holds the window band (18 key tiles per row) but not the
+    # 18 extra tiles for vision spans past a row's causal end: query tiles whose
+    # vision spans reach past the band are recomputed in the second dQ launch.
+    lq = lk = [2600]
+    q, k, v, do, dlse = qkv(9300, 2600, 2600, 32, 16, 256)
+    cq, ck = cu(lq), cu(lk)
+    vis = torch.full((2600,), -1, dtype=torch.int32)
+    vis[400:1500] = 0  # a 1100-token block: its early rows reach far past the band
+    vis[1800:2100] = 1
+    rows = 2600 // 32 + 1
+    band = rows * 18 * 32 * 4096
+    got, plan = _stages(q, k, v, do, dlse, cq, ck, 1024, vis=vis, ds_budget=band + 4096)
+    full = plan.workspace_bytes(1)
+    plan.ds_budget = -1
+    assert full - plan.workspace_bytes(1) == band  # only the band is stored
+    (o_ref, l_ref, *refs), bf = _oracle(q, k, v, do, dlse, cq, ck, 1024, vis)
+    check_forward(got[0], got[1], o_ref, l_ref, local=True, label="partial band")
+    check_gradients(got[2:], refs, bf, label="partial band")
+
+
+def test_global_sequence_past_the_default_ds_budget():
+    import gemma4_fa4_amd as g
+
+    s = 16448  # 514 rows x 257 key tiles x 32 heads x 4 KB > 16 GiB: no stored dS
+    print(f"global S={s} through fa4_global_varlen_forward", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(16448)
+    sd = 512 ** -0.25
+    q = (torch.randn(s, 32, 512, generator=gen, device=DEV) * sd).to(torch.bfloat16)
+    k = (torch.randn(s, 4, 512, generator=gen, device=DEV) * sd).to(torch.bfloat16)
+    v = torch.randn(s, 4, 512, generator=gen, device=DEV).to(torch.bfloat16)
+    do = torch.randn(s, 32, 512, generator=gen, device=DEV).to(torch.bfloat16)
+    c = torch.tensor([0, s], dtype=torch.int32, device=DEV)
+    qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o, lse = g.fa4_global_varlen_forward(qd, kd, vd, c, c, max_seqlen_q=s, max_seqlen_k=s)
+    torch.autograd.backward(o, do)
+    torch.cuda.synchronize()
+    from gemma4_fa4_amd.attention import _packed_plan
+
+    plan = _packed_plan(q, k, c, c, s, s, g.GLOBAL_ATTENTION)
+    assert _workspace_has_no_ds(plan)
+    heads = list(range(8, 16))  # KV group 1 in full, so its dK/dV are complete
+    cc = [0, s]
+    o_ref, l_ref, dq_ref, dk_ref, dv_ref = attention_fwd_bwd(
+        q, k, v, cc, cc, do=do, compute_dtype=torch.float64, heads=heads, q_chunk=1024)
+    _, bq, bk, bv = bf16_baseline_fwd_bwd(q, k, v, cc, cc, do=do, heads=heads, q_chunk=512)
+    h = slice(8, 16)
+    check_forward(o.detach()[:, h], lse.detach()[h], o_ref[:, h].cpu(), l_ref[h].cpu(),
+                  local=False, label="S16448")
+    check_gradients(
+        [qd.grad[:, h], kd.grad[:, 1:2], vd.grad[:, 1:2]],
+        [dq_ref[:, h].cpu(), dk_ref[:, 1:2].cpu(), dv_ref[:, 1:2].cpu()],
+        [bq[:, h].cpu(), bk[:, 1:2].cpu(), bv[:, 1:2].cpu()], label="S16448")

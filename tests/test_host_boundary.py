@@ -282,3 +282,33 @@ def test_model_contract_constants():
     assert len(types) == 60 and types.count("full_attention") == 10
     assert types[5] == "full_attention" and types[4] == "sliding_attention"
     assert f.rotary_dim == 128 and f.qhead_per_kvhead == 8 and s.qhead_per_kvhead == 2
+
+
+def test_cumulative_host_copies_are_reused_only_while_unchanged(monkeypatch):
+    cache = att._HostValues(capacity=2)
+    monkeypatch.setattr(att, "_CU_HOST", cache)
+    copies = []
+    real_cpu = torch.Tensor.cpu
+
+    def counting_cpu(self, *a, **kw):
+        copies.append(1)
+        return real_cpu(self, *a, **kw)
+
+    monkeypatch.setattr(torch.Tensor, "cpu", counting_cpu)
+    cu = torch.tensor([0, 5, 9], dtype=torch.int32)
+    assert att._host_values(cu, cu) == ([0, 5, 9], [0, 5, 9]) and len(copies) == 1
+    assert att._host_values(cu, cu) == ([0, 5, 9], [0, 5, 9]) and len(copies) == 1
+    cu[1] = 4  # in-place change: read again
+    assert att._host_values(cu, cu)[0] == [0, 4, 9] and len(copies) == 2
+    cu.view(3)[2].add_(1)  # through a view
+    assert att._host_values(cu, cu)[0] == [0, 4, 10] and len(copies) == 3
+    other = cu.clone()  # equal values, different tensor: read
+    assert att._host_values(other, other)[0] == [0, 4, 10] and len(copies) == 4
+    cq, ck = torch.tensor([0, 3], dtype=torch.int32), torch.tensor([0, 7], dtype=torch.int32)
+    assert att._host_values(cq, ck) == ([0, 3], [0, 7]) and len(copies) == 5
+    assert att._host_values(cq, ck) == ([0, 3], [0, 7]) and len(copies) == 5
+    with torch.inference_mode():
+        inf = torch.tensor([0, 2], dtype=torch.int32)
+    att._host_values(inf, inf)
+    att._host_values(inf, inf)
+    assert len(copies) == 7  # inference tensors are always read

@@ -94,3 +94,39 @@ def test_workloads_are_seed_deterministic():
     t1 = wl.tensors(wl.config1(), "cpu")
     t2 = wl.tensors(wl.config1(), "cpu")
     assert all((x is None and y is None) or bool((x == y).all()) for x, y in zip(t1, t2))
+
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("with_docs", [False, True])
+def test_allowed_intervals_are_the_mask_rows(seed, with_docs, monkeypatch):
+    # Every row of the oracle's mask is one interval [lo, hi] of the packed
+    # key stream (the Q=0 closed forms of the full-size GPU tests rely on it).
+    import torch
+
+    from oracle.masks import gemma4_attention_mask
+
+    lengths = [37, 1, 90, 64]
+    w = _small(seed, "local", lengths, vision_frac=True, with_docs=with_docs)
+    monkeypatch.setattr(wl.Workload, "window", property(lambda self: 16))
+    lo, hi = wl.allowed_intervals(w)
+    cu = w.cu()
+    for s in range(len(lengths)):
+        a, b = cu[s], cu[s + 1]
+        mask = gemma4_attention_mask(
+            batch_size=1, q_len=b - a, kv_len=b - a, sliding_window=16,
+            vision_block_ids=torch.from_numpy(w.vision[a:b])[None],
+            document_ids=None if w.documents is None else torch.from_numpy(w.documents[a:b])[None],
+            allow_vision_bidirectional=True)[0, 0].numpy()
+        for i in range(b - a):
+            row = np.nonzero(mask[i])[0]
+            assert row[0] == lo[a + i] - a and row[-1] == hi[a + i] - a
+            assert len(row) == row[-1] - row[0] + 1
+
+
+def test_allowed_intervals_of_a_global_workload_are_causal_prefixes():
+    w = wl.config4()
+    lo, hi = wl.allowed_intervals(w)
+    cu = w.cu()
+    for s in range(len(w.seg_lengths)):
+        assert np.all(lo[cu[s]: cu[s + 1]] == cu[s])
+        assert np.array_equal(hi[cu[s]: cu[s + 1]], np.arange(cu[s], cu[s + 1]))
