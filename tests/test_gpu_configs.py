@@ -77,12 +77,13 @@ def _check_sampled_heads(w, tensors, outs):
         label = f"{w.name} group {g}"
         fro, lse_err = check_forward(o[:, h], lse[h], o_r[:, h].cpu(), l_r[h].cpu(),
                                      local=w.kind == "local", label=label)
-        rep = check_gradients([dq[:, h], dk[:, gs], dv[:, gs]],
-                              [dq_r[:, h].cpu(), dk_r[:, gs].cpu(), dv_r[:, gs].cpu()],
-                              [bq[:, h].cpu(), bk[:, gs].cpu(), bv[:, gs].cpu()], label=label)
+        report = check_gradients([dq[:, h], dk[:, gs], dv[:, gs]],
+                                 [dq_r[:, h].cpu(), dk_r[:, gs].cpu(), dv_r[:, gs].cpu()],
+                                 [bq[:, h].cpu(), bk[:, gs].cpu(), bv[:, gs].cpu()],
+                                 label=label)
         print(f"  O rel-fro {fro:.2e}, LSE max-abs {lse_err:.2e}, " + ", ".join(
             f"{n} max-abs {e:.2e} (limit {lim:.2e}) rel-fro {f:.2e}"
-            for n, (e, lim, f) in rep.items()), flush=True)
+            for n, (e, lim, f) in report.items()), flush=True)
         del o_r, l_r, dq_r, dk_r, dv_r, bq, bk, bv
         torch.cuda.empty_cache()
 
