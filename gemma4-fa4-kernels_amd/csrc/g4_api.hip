@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include <algorithm>
@@ -106,6 +107,81 @@ unsigned* sched_ptr(const g4_problem& p, void* ws) {
                      g4::delta_bytes(p) + g4::ds_bytes(p));
 }
 
+// Forward workspace of g4_attn_fwd_static: a file-scope device array, one
+// copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol);
+// it uses the per-device address hipGetSymbolAddress returns.
+constexpr size_t kStaticWorkspaceBytes = size_t(32) << 20;
+static_assert(kStaticWorkspaceBytes == G4_STATIC_WORKSPACE_BYTES, "header and library agree");
+__device__ __align__(256) unsigned char scratch[kStaticWorkspaceBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` on each GPU, once looked up
+
+// Address of `scratch` on the device `stream` belongs to (looked up once per
+// device, with that device current).
+int scratch_for_stream(hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipStreamGetDevice(stream, &dev);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(G4_ERR_UNSUPPORTED, "device ordinal out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = 0;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    void* ptr = nullptr;
+    const hipError_t ge = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev && (e = hipSetDevice(cur)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    if (ge != hipSuccess) return hip_fail(ge, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr || ((uintptr_t)ptr) % 256)
+      return fail(G4_ERR_LAUNCH, "static workspace address is not 256-byte aligned");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return G4_OK;
+}
+
+int fwd_impl(const g4_problem* p, const void* q, g4_layout ql, const void* k, g4_layout kl,
+             const void* v, g4_layout vl, void* o, g4_layout ol, float* lse, void* ws,
+             hipStream_t st) {
+  g4::FwdParams a{};
+  a.p = *p;
+  a.q = (const __bf16*)q;
+  a.k = (const __bf16*)k;
+  a.v = (const __bf16*)v;
+  a.o = (__bf16*)o;
+  a.lse = lse;
+  a.ql = ql;
+  a.kl = kl;
+  a.vl = vl;
+  a.ol = ol;
+  a.num_seqs = p->num_seqs;
+  if (g4::spans_bytes(*p)) {
+    hipError_t e = g4::launch_spans(*p, ws, st);
+    if (e != hipSuccess) return hip_fail(e, "span table");
+  }
+  g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);
+  a.raise_flags = raise_flags_ptr(*p, ws);
+  hipError_t e = g4::launch_fwd(a, st);
+  if (e != hipSuccess) return hip_fail(e, "forward");
+  return G4_OK;
+}
+
+int check_fwd_operands(const g4_problem* p, const void* q, g4_layout ql, const void* k,
+                       g4_layout kl, const void* v, g4_layout vl, const void* o, g4_layout ol,
+                       const float* lse) {
+  G4_TRY(check_problem(p));
+  G4_TRY(check_operand(q, ql, "q"));
+  G4_TRY(check_operand(k, kl, "k"));
+  G4_TRY(check_operand(v, vl, "v"));
+  G4_TRY(check_operand(o, ol, "o"));
+  if (lse == nullptr) return fail(G4_ERR_INVALID, "lse is NULL");
+  return G4_OK;
+}
+
 }  // namespace
 
 namespace g4 {
@@ -180,35 +256,25 @@ int g4_attn_fwd(const g4_problem* p, const void* q, g4_layout ql, const void* k,
                 const void* v, g4_layout vl, void* o, g4_layout ol, float* lse, void* ws,
                 size_t ws_bytes, void* stream) {
   g_last_error.clear();
-  G4_TRY(check_problem(p));
-  G4_TRY(check_operand(q, ql, "q"));
-  G4_TRY(check_operand(k, kl, "k"));
-  G4_TRY(check_operand(v, vl, "v"));
-  G4_TRY(check_operand(o, ol, "o"));
-  if (lse == nullptr) return fail(G4_ERR_INVALID, "lse is NULL");
+  G4_TRY(check_fwd_operands(p, q, ql, k, kl, v, vl, o, ol, lse));
   G4_TRY(check_ws(p, 0, ws, ws_bytes));
-  hipStream_t st = (hipStream_t)stream;
-  g4::FwdParams a{};
-  a.p = *p;
-  a.q = (const __bf16*)q;
-  a.k = (const __bf16*)k;
-  a.v = (const __bf16*)v;
-  a.o = (__bf16*)o;
-  a.lse = lse;
-  a.ql = ql;
-  a.kl = kl;
-  a.vl = vl;
-  a.ol = ol;
-  a.num_seqs = p->num_seqs;
-  if (g4::spans_bytes(*p)) {
-    hipError_t e = g4::launch_spans(*p, ws, st);
-    if (e != hipSuccess) return hip_fail(e, "span table");
+  return fwd_impl(p, q, ql, k, kl, v, vl, o, ol, lse, ws, (hipStream_t)stream);
+}
+
+int g4_attn_fwd_static(const g4_problem* p, const void* q, g4_layout ql, const void* k,
+                       g4_layout kl, const void* v, g4_layout vl, void* o, g4_layout ol,
+                       float* lse, void* stream) {
+  g_last_error.clear();
+  G4_TRY(check_fwd_operands(p, q, ql, k, kl, v, vl, o, ol, lse));
+  const size_t need = g4_workspace_bytes(p, 0);
+  if (need > kStaticWorkspaceBytes) {
+    char buf[160];
+    snprintf(buf, sizeof buf, "%zu bytes needed, %zu available", need, kStaticWorkspaceBytes);
+    return fail(G4_ERR_WORKSPACE, "problem exceeds the static forward workspace: %s", buf);
   }
-  g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);
-  a.raise_flags = raise_flags_ptr(*p, ws);
-  hipError_t e = g4::launch_fwd(a, st);
-  if (e != hipSuccess) return hip_fail(e, "forward");
-  return G4_OK;
+  void* ws = nullptr;
+  G4_TRY(scratch_for_stream((hipStream_t)stream, &ws));
+  return fwd_impl(p, q, ql, k, kl, v, vl, o, ol, lse, ws, (hipStream_t)stream);
 }
 
 static int fill_bwd(g4::BwdParams& a, const g4_problem* p, const void* q, g4_layout ql,

@@ -24,12 +24,14 @@ G4_ERR_INVALID = 1
 G4_ERR_UNSUPPORTED = 2
 G4_ERR_WORKSPACE = 3
 G4_ERR_LAUNCH = 4
+STATIC_WORKSPACE_BYTES = 32 << 20  # G4_STATIC_WORKSPACE_BYTES
 
 EXPORTED_SYMBOLS = (
     "g4_abi_version",
     "g4_last_error",
     "g4_workspace_bytes",
     "g4_attn_fwd",
+    "g4_attn_fwd_static",
     "g4_attn_bwd",
     "g4_attn_bwd_delta",
     "g4_attn_bwd_dkdv",
@@ -79,6 +81,7 @@ _SIGNATURES = {
     "g4_last_error": (ctypes.c_char_p, []),
     "g4_workspace_bytes": (ctypes.c_size_t, [_PROB, ctypes.c_int]),
     "g4_attn_fwd": (ctypes.c_int, [_PROB, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _SZ, _P]),
+    "g4_attn_fwd_static": (ctypes.c_int, [_PROB, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P]),
     "g4_attn_bwd": (
         ctypes.c_int,
         [_PROB, _P, _L, _P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _P, _L, _P, _L, _P, _L, _P, _SZ, _P],

@@ -112,6 +112,30 @@ int g4_attn_fwd(const g4_problem* p,
                 void* stream);
 
 /*
+ * Forward exactly as g4_attn_fwd (same kernels, same results), with the
+ * workspace taken from the library's own device memory instead of a caller
+ * buffer.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The workspace is a file-scope device
+ * array of G4_STATIC_WORKSPACE_BYTES, one per GPU, held until the process
+ * ends; its address on the stream's GPU is looked up on the first call there.
+ * Problems whose forward workspace (g4_workspace_bytes(p, 0): the vision span
+ * tables, 40 bytes per K token with vision IDs, and the head-dim 512 pass
+ * flags, 4 bytes per 32 queries per head) exceeds it are rejected with
+ * G4_ERR_WORKSPACE.  Every call on a GPU uses the same array: calls that
+ * overlap on one GPU (other streams, other threads) race; calls on one stream
+ * are ordered and safe.  Allocates nothing, no host synchronisation.
+ */
+#define G4_STATIC_WORKSPACE_BYTES (32u << 20)
+int g4_attn_fwd_static(const g4_problem* p,
+                       const void* q, g4_layout q_layout,
+                       const void* k, g4_layout k_layout,
+                       const void* v, g4_layout v_layout,
+                       void* o, g4_layout o_layout,
+                       float* lse,
+                       void* stream);
+
+/*
  * Backward: dQ, dK, dV given O, dO, LSE and optional dLSE (same layout as LSE,
  * NULL = zero).  dK and dV are distinct outputs; no atomics (bitwise
  * repeatable).  Runs g4_attn_bwd_delta, g4_attn_bwd_dkdv and g4_attn_bwd_dq.

@@ -312,3 +312,22 @@ def test_cumulative_host_copies_are_reused_only_while_unchanged(monkeypatch):
     att._host_values(inf, inf)
     att._host_values(inf, inf)
     assert len(copies) == 7  # inference tensors are always read
+
+
+def test_static_workspace_forward_rejects_a_problem_beyond_its_array():
+    # Host-side check before any device call: vision span tables of 2^20 K
+    # tokens need 40 MiB, more than the 32 MiB static forward workspace.
+    import ctypes
+    lib = _lib.load()
+    t = 1 << 20
+    p = _lib.G4Problem(num_seqs=1, seqlen_q=t, seqlen_k=t, num_q_heads=32, num_kv_heads=16,
+                       head_dim=256, window=1024, bidirectional_vision=1, total_q=t, total_k=t,
+                       cu_seqlens_q=0x1000, cu_seqlens_k=0x1000, vision_ids=0x2000,
+                       lse_head_stride=t)
+    assert lib.g4_workspace_bytes(ctypes.byref(p), 0) > _lib.STATIC_WORKSPACE_BYTES
+    lay = _lib.G4Layout(0, 32 * 256, 256)
+    kv = _lib.G4Layout(0, 16 * 256, 256)
+    rc = lib.g4_attn_fwd_static(ctypes.byref(p), 0x10000, lay, 0x20000, kv, 0x30000, kv,
+                                0x40000, lay, 0x50000, None)
+    assert rc == _lib.G4_ERR_WORKSPACE
+    assert b"static forward workspace" in lib.g4_last_error()
