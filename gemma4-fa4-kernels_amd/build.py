@@ -16,7 +16,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_DIR = os.path.join(HERE, "gemma4_fa4_amd", "_lib")
 LIB = os.path.join(LIB_DIR, "libgemma4_attn.so")
-SOURCES = ["g4_api.hip", "g4_meta.hip", "g4_fwd.hip", "g4_bwd.hip", "g4_bwd_roles.hip"]
+SOURCES = ["g4_api.hip", "g4_meta.hip", "g4_fwd.hip", "g4_bwd.hip", "g4_bwd_roles.hip",
+           "g4_kvprep.hip"]
 ARCH = "gfx950"
 FLAGS = [
     "-O3",

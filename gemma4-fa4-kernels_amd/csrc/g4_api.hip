@@ -398,6 +398,85 @@ int g4_mask_materialize(const g4_problem* p, uint8_t* out, void* ws, size_t ws_b
   return G4_OK;
 }
 
+static int check_kv_prep(const g4_kv_prep* p) {
+  if (p == nullptr) return fail(G4_ERR_INVALID, "K/V preparation descriptor is NULL");
+  if (p->num_batches < 1 || p->seqlen < 1 || p->num_heads < 1)
+    return fail(G4_ERR_INVALID, "num_batches, seqlen and num_heads must be >= 1");
+  if (p->head_dim != 512)
+    return fail(G4_ERR_UNSUPPORTED, "K/V preparation supports head_dim 512 (the global layer)");
+  if (p->rotary_dim < 0 || p->rotary_dim > p->head_dim || p->rotary_dim % 16)
+    return fail(G4_ERR_INVALID, "rotary_dim must be a multiple of 16 in [0, head_dim]");
+  if (!(p->eps >= 0.f) || p->eps > 1.f) return fail(G4_ERR_INVALID, "eps must be in [0, 1]");
+  if (p->cs_batch_stride < 0 || p->cs_batch_stride % 4)
+    return fail(G4_ERR_INVALID, "cs_batch_stride must be a non-negative multiple of 4");
+  if (p->k_fp32 != 0 && p->k_fp32 != 1) return fail(G4_ERR_INVALID, "k_fp32 must be 0 or 1");
+  return G4_OK;
+}
+
+static int check_prep_operand(const void* ptr, const g4_layout& l, const char* name) {
+  if (ptr == nullptr) return fail(G4_ERR_INVALID, "operand %s is NULL", name);
+  if (((uintptr_t)ptr) % 16) return fail(G4_ERR_INVALID, "operand %s must be 16-byte aligned", name);
+  if (l.token_stride <= 0 || l.head_stride <= 0 || l.batch_stride < 0 || l.token_stride % 8 ||
+      l.head_stride % 8 || l.batch_stride % 8)
+    return fail(G4_ERR_INVALID, "operand %s strides must be multiples of 8 elements", name);
+  return G4_OK;
+}
+
+static int check_prep_tables(const g4_kv_prep* p, const float* w, const float* c, const float* s) {
+  if (w == nullptr || ((uintptr_t)w) % 16)
+    return fail(G4_ERR_INVALID, "weight must be a 16-byte aligned fp32 array");
+  if (p->rotary_dim > 0 && (c == nullptr || s == nullptr || ((uintptr_t)c) % 16 ||
+                            ((uintptr_t)s) % 16))
+    return fail(G4_ERR_INVALID, "cos and sin must be 16-byte aligned fp32 arrays");
+  return G4_OK;
+}
+
+int g4_kv_prep_fwd(const g4_kv_prep* p, const void* z, g4_layout zl, const float* weight,
+                   const float* cosv, const float* sinv, void* k, g4_layout kl, void* v,
+                   g4_layout vl, void* stream) {
+  g_last_error.clear();
+  G4_TRY(check_kv_prep(p));
+  G4_TRY(check_prep_operand(z, zl, "z"));
+  G4_TRY(check_prep_operand(k, kl, "k"));
+  G4_TRY(check_prep_operand(v, vl, "v"));
+  G4_TRY(check_prep_tables(p, weight, cosv, sinv));
+  hipError_t e = g4::launch_kv_prep_fwd(*p, z, zl, weight, cosv, sinv, k, kl, v, vl,
+                                        (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "K/V preparation forward");
+  return G4_OK;
+}
+
+size_t g4_kv_prep_workspace_bytes(const g4_kv_prep* p) {
+  g_last_error.clear();
+  if (check_kv_prep(p) != G4_OK) return 0;
+  return g4::kv_prep_workspace_bytes(*p);
+}
+
+int g4_kv_prep_bwd(const g4_kv_prep* p, const void* z, g4_layout zl, const float* weight,
+                   const float* cosv, const float* sinv, const void* dk, g4_layout dkl,
+                   const void* dv, g4_layout dvl, void* dz, g4_layout dzl, float* dweight,
+                   void* ws, size_t ws_bytes, void* stream) {
+  g_last_error.clear();
+  G4_TRY(check_kv_prep(p));
+  G4_TRY(check_prep_operand(z, zl, "z"));
+  G4_TRY(check_prep_operand(dk, dkl, "dk"));
+  G4_TRY(check_prep_operand(dv, dvl, "dv"));
+  G4_TRY(check_prep_operand(dz, dzl, "dz"));
+  G4_TRY(check_prep_tables(p, weight, cosv, sinv));
+  if (dweight == nullptr || ((uintptr_t)dweight) % 16)
+    return fail(G4_ERR_INVALID, "dweight must be a 16-byte aligned fp32 array");
+  const size_t need = g4::kv_prep_workspace_bytes(*p);
+  if (ws_bytes < need || ws == nullptr || ((uintptr_t)ws) % 16) {
+    char buf[128];
+    snprintf(buf, sizeof buf, "%zu aligned bytes needed, %zu given", need, ws_bytes);
+    return fail(G4_ERR_WORKSPACE, "K/V preparation workspace: %s", buf);
+  }
+  hipError_t e = g4::launch_kv_prep_bwd(*p, z, zl, weight, cosv, sinv, dk, dkl, dv, dvl, dz, dzl,
+                                        dweight, ws, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "K/V preparation backward");
+  return G4_OK;
+}
+
 int g4_tile_ranges(const g4_problem* p, int direction, int row_tile, int32_t* out, void* ws,
                    size_t ws_bytes, void* stream) {
   g_last_error.clear();

@@ -120,4 +120,14 @@ hipError_t launch_mask(const g4_problem& p, uint8_t* out, const int* span_lo, co
 hipError_t launch_ranges(const g4_problem& p, int direction, int row_tile, int32_t* out,
                          const int* span_lo, const int* span_hi, hipStream_t stream);
 
+// K/V preparation from the shared projection source (g4_kvprep.hip).
+size_t kv_prep_workspace_bytes(const g4_kv_prep& p);
+hipError_t launch_kv_prep_fwd(const g4_kv_prep& p, const void* z, g4_layout zl, const float* w,
+                              const float* cosv, const float* sinv, void* k, g4_layout kl,
+                              void* v, g4_layout vl, hipStream_t stream);
+hipError_t launch_kv_prep_bwd(const g4_kv_prep& p, const void* z, g4_layout zl, const float* w,
+                              const float* cosv, const float* sinv, const void* dk,
+                              g4_layout dkl, const void* dv, g4_layout dvl, void* dz,
+                              g4_layout dzl, float* dw, void* ws, hipStream_t stream);
+
 }  // namespace g4

@@ -16,6 +16,7 @@ from .attention import (
     fa4_local_varlen_forward,
 )
 from .errors import GlobalBackwardBudgetExceeded, UnsupportedH100Path, UnsupportedMI355XPath
+from .kv_prep import prepare_global_kv_from_projection_source
 from .model_spec import (
     GEMMA4_31B,
     GLOBAL_ATTENTION,
@@ -47,6 +48,7 @@ __all__ = [
     "fa4_global_forward_only",
     "fa4_global_varlen_forward",
     "fa4_global_varlen_forward_only",
+    "prepare_global_kv_from_projection_source",
     "GlobalBackwardBudgetExceeded",
     "UnsupportedH100Path",
     "UnsupportedMI355XPath",

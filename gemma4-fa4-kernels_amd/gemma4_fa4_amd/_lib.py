@@ -38,6 +38,9 @@ EXPORTED_SYMBOLS = (
     "g4_attn_bwd_dq",
     "g4_mask_materialize",
     "g4_tile_ranges",
+    "g4_kv_prep_fwd",
+    "g4_kv_prep_workspace_bytes",
+    "g4_kv_prep_bwd",
 )
 
 
@@ -71,9 +74,23 @@ class G4Problem(ctypes.Structure):
     ]
 
 
+class G4KvPrep(ctypes.Structure):
+    _fields_ = [
+        ("num_batches", ctypes.c_int32),
+        ("seqlen", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("rotary_dim", ctypes.c_int32),
+        ("k_fp32", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("cs_batch_stride", ctypes.c_int64),
+    ]
+
+
 _P = ctypes.c_void_p
 _L = G4Layout
 _PROB = ctypes.POINTER(G4Problem)
+_PREP = ctypes.POINTER(G4KvPrep)
 _SZ = ctypes.c_size_t
 
 _SIGNATURES = {
@@ -97,6 +114,12 @@ _SIGNATURES = {
     ),
     "g4_mask_materialize": (ctypes.c_int, [_PROB, _P, _P, _SZ, _P]),
     "g4_tile_ranges": (ctypes.c_int, [_PROB, ctypes.c_int, ctypes.c_int, _P, _P, _SZ, _P]),
+    "g4_kv_prep_fwd": (ctypes.c_int, [_PREP, _P, _L, _P, _P, _P, _P, _L, _P, _L, _P]),
+    "g4_kv_prep_workspace_bytes": (ctypes.c_size_t, [_PREP]),
+    "g4_kv_prep_bwd": (
+        ctypes.c_int,
+        [_PREP, _P, _L, _P, _P, _P, _P, _L, _P, _L, _P, _L, _P, _P, _SZ, _P],
+    ),
 }
 
 _lock = threading.Lock()

@@ -220,6 +220,60 @@ int g4_mask_materialize(const g4_problem* p, uint8_t* out,
 int g4_tile_ranges(const g4_problem* p, int direction, int row_tile, int32_t* out,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Global-layer K/V preparation from the shared projection source (the
+ * reference's prepare_global_kv_from_projection_source,
+ * src/gemma4_fa4/reference.py:306-328, with rms_norm 276-281 and partial
+ * RoPE 284-303; design note docs/design.md:202-213).  Per (batch, token,
+ * head) row z of head_dim elements:
+ *   r = (mean(z^2) + eps)^(-1/2), n = z r               (fp32)
+ *   V = bf16(n)                                          (RMSNorm, no weight)
+ *   kn = bf16(n w); K = kn with RoPE on its first rotary_dim dims
+ *        (K_i = kn_i cos_i + rot(kn)_i sin_i, rot(x) = (-x2, x1) over the
+ *        rotary dims, fp32 products and sum), other dims unchanged.
+ * K is written as bf16, or as fp32 with k_fp32 = 1 (the dtype the reference
+ * returns for a bf16 source and fp32 cos / sin).  Z, K, V, dZ use g4_layout
+ * element strides (K's in its own dtype); rows are (batch, token, head).
+ * cos / sin are fp32 (batch, seqlen, rotary_dim), rows contiguous, batch
+ * stride cs_batch_stride elements (0: shared by every batch); the weight is
+ * fp32 of head_dim.  head_dim must be 512; rotary_dim a multiple of 16 up to
+ * 512.
+ */
+typedef struct g4_kv_prep {
+  int32_t num_batches;
+  int32_t seqlen;
+  int32_t num_heads;
+  int32_t head_dim;
+  int32_t rotary_dim;
+  int32_t k_fp32;
+  float eps;
+  int64_t cs_batch_stride;
+} g4_kv_prep;
+
+/* Forward: K, V from the source.  Stream-ordered, no workspace. */
+int g4_kv_prep_fwd(const g4_kv_prep* p,
+                   const void* z, g4_layout z_layout,
+                   const float* weight, const float* cos, const float* sin,
+                   void* k, g4_layout k_layout,
+                   void* v, g4_layout v_layout,
+                   void* stream);
+
+/* Workspace bytes of g4_kv_prep_bwd (per-workgroup partial sums of dweight). */
+size_t g4_kv_prep_workspace_bytes(const g4_kv_prep* p);
+
+/* Backward: dZ (bf16) and dweight (fp32, head_dim, overwritten) from dK (in
+ * K's dtype) and dV (bf16) through both preparation adjoints; no atomics,
+ * bitwise repeatable. */
+int g4_kv_prep_bwd(const g4_kv_prep* p,
+                   const void* z, g4_layout z_layout,
+                   const float* weight, const float* cos, const float* sin,
+                   const void* dk, g4_layout dk_layout,
+                   const void* dv, g4_layout dv_layout,
+                   void* dz, g4_layout dz_layout,
+                   float* dweight,
+                   void* workspace, size_t workspace_bytes,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -114,7 +114,7 @@ def test_local_varlen_backward(lq, lk, meta):
     check_gradients([qd.grad, kd.grad, vd.grad], refs, bf, label=f"local varlen {lq}")
 
 
-@pytest.mark.parametrize("s", [1, 33, 65, 129, 1000, 2048])
+@pytest.mark.parametrize("s", [1, 33, 65, 129, 511, 512, 513, 1000, 1024, 2048])
 def test_global_text_backward(s):
     g = _g()
     q, k, v, do, dlse = qkv(4000 + s, s, s, 32, 4, 512)
@@ -150,6 +150,33 @@ def test_backward_is_bitwise_repeatable():
         ((o.float() * do[None].to(DEV).float()).sum() + (lse * dlse[None].to(DEV)).sum()).backward()
         out.append([t.grad.clone() for t in (qd, kd, vd)])
     for a, b in zip(*out):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("layer", ["local", "global"])
+def test_backward_is_bitwise_repeatable_on_a_side_stream(layer):
+    # test_h100_fa4.py:2240-2249 repeats on a non-default stream: the forward and
+    # backward launched on a side stream equal the default-stream results bit for bit.
+    g = _g()
+    s = 1025 if layer == "local" else 700
+    hkv, d = (16, 256) if layer == "local" else (4, 512)
+    fn = g.fa4_local_text_forward if layer == "local" else g.fa4_global_text_forward
+    q, k, v, do, dlse = qkv(6100, s, s, 32, hkv, d)
+
+    def run():
+        qd, kd, vd = (t[None].to(DEV).requires_grad_(True) for t in (q, k, v))
+        o, lse = fn(qd, kd, vd)
+        ((o.float() * do[None].to(DEV).float()).sum()
+         + (lse * dlse[None].to(DEV)).sum()).backward()
+        return [t.detach().clone() for t in (o, lse, qd.grad, kd.grad, vd.grad)]
+
+    ref = run()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        got = run()
+    side.synchronize()
+    for a, b in zip(ref, got):
         assert torch.equal(a, b)
 
 

@@ -14,7 +14,7 @@ def _g():
     return g
 
 
-@pytest.mark.parametrize("s", [1, 2, 31, 63, 64, 65, 127, 128, 129, 255, 1024, 1025])
+@pytest.mark.parametrize("s", [1, 2, 31, 63, 64, 65, 127, 128, 129, 255, 1023, 1024, 1025])
 def test_local_text_fixed(s):
     g = _g()
     q, k, v, _, _ = qkv(100 + s, s, s, **{k_: LOCAL[k_] for k_ in ("hq", "hkv", "d")})
@@ -71,7 +71,8 @@ def test_local_varlen(lq, lk, meta):
     check_forward(o, lse, o_ref, l_ref, local=True, label=f"local varlen {lq}/{lk}")
 
 
-@pytest.mark.parametrize("s", [1, 31, 32, 33, 63, 64, 65, 127, 128, 129, 1000, 2048])
+@pytest.mark.parametrize("s", [1, 31, 32, 33, 63, 64, 65, 127, 128, 129, 511, 512, 513, 1000,
+                               1024, 2048])
 def test_global_text_fixed(s):
     g = _g()
     q, k, v, _, _ = qkv(300 + s, s, s, 32, 4, 512)
