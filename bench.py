@@ -211,6 +211,50 @@ def kernel_roofline(torch, g, tensors, *, s: int, reps: int):
     return roofline, per_kernel, round(delta_gbs, 1), round(2 * CALIBRATION_COPY_BYTES / copy_ms / 1e6, 1)
 
 
+def kv_prep_timing(torch, dev, reps: int):
+    """Fused global K/V preparation at configuration 2's K/V shape, against the HBM roofline.
+
+    Source (1, 4, 8192, 512) bf16, fp32 cos / sin over 128 rotary dims (K in
+    fp32, V in bf16) and bf16 tables (K and V in bf16, the attention's input).
+    Algorithmic bytes: forward reads Z, cos, sin, the weight and writes K, V;
+    backward reads Z, dK, dV, cos, sin, the weight and writes dZ (plus the
+    per-workgroup dweight partials, written and read once).
+    """
+    import gemma4_fa4_amd as g
+
+    b, h, s, d, rot = 1, 4, 8192, 512, 128
+    gen = torch.Generator(device=dev).manual_seed(7)
+    z = torch.randn(b, h, s, d, generator=gen, device=dev).to(torch.bfloat16)
+    w = torch.rand(d, generator=gen, device=dev) + 0.5
+    ang = torch.rand(b, s, rot, generator=gen, device=dev)
+    out = {}
+    for label, tdt in (("k_fp32", torch.float32), ("k_bf16", torch.bfloat16)):
+        cos, sin = torch.cos(ang).to(tdt), torch.sin(ang).to(tdt)
+        zr = z.detach().requires_grad_(True)
+        wr = w.detach().requires_grad_(True)
+        k, v = g.prepare_global_kv_from_projection_source(zr, k_norm_weight=wr, cos=cos, sin=sin)
+        dk, dv = torch.randn_like(k), torch.randn_like(v)
+        kb = k.element_size()
+        fwd_ms = statistics.median(event_times(torch, lambda: g.prepare_global_kv_from_projection_source(
+            z, k_norm_weight=w, cos=cos, sin=sin), reps, 2))
+        bwd_ms = statistics.median(event_times(
+            torch, lambda: torch.autograd.backward((k, v), (dk, dv), retain_graph=True), reps, 2))
+        n = b * h * s * d
+        tables = 2 * b * s * rot * cos.element_size()
+        fwd_bytes = n * 2 + tables + d * 4 + n * kb + n * 2
+        parts = min((b * h * s + 3) // 4, 2048) * d * 4
+        bwd_bytes = n * 2 + n * kb + n * 2 + tables + d * 4 + n * 2 + 2 * parts + d * 4
+        out[label] = {
+            "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+            "fwd_gbs": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9, 1),
+            "bwd_gbs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1),
+            "fwd_frac_hbm": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
+            "bwd_frac_hbm": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
+            "fwd_bytes": fwd_bytes, "bwd_bytes": bwd_bytes,
+        }
+    return out
+
+
 def kernel_source_digest() -> str:
     """SHA-256 over the HIP sources, so recorded counters are tied to the kernels measured."""
     h = hashlib.sha256()
@@ -359,6 +403,7 @@ def main() -> int:
             head["fwd_bwd_cold_ms"] = cold["fwd_bwd_ms"]
             head["fwd_bwd_cold_tflops"] = cold["fwd_bwd_tflops"]
             del junk
+        extra["kv_prep_global_S8192_4heads"] = kv_prep_timing(torch, dev, max(5, args.steps))
         chosen = [int(x) for x in args.extra_configs.split(",") if x.strip()]
         for cfg in (getattr(wl, f"config{i}") for i in chosen if i != 2):
             w = cfg()
