@@ -706,8 +706,39 @@ def _backward_additional_bytes(plan: _Plan, q, k, v) -> int:
     return grads + plan.workspace_bytes(1)
 
 
+def _fit_ds_budget(plan: _Plan, q, k, v, budget: int) -> int:
+    """Fit the backward's stored dS tiles to ``budget`` bytes of additional HBM.
+
+    The MI355X counterpart of the reference's budget fallback
+    (transformers_integration.py:1950-1961, which re-runs a low-memory
+    composition when the native global backward exceeds its budget): the
+    dK/dV stage stores dS tiles only while they fit what the budget leaves after
+    the gradients and the O(T) part of the workspace; past that the dQ stage
+    recomputes S and dP.  Returns the additional bytes the backward will need.
+    """
+    plan.ds_budget = 0
+    full = _backward_additional_bytes(plan, q, k, v)
+    if full <= budget:
+        return full
+    plan.ds_budget = -1
+    lean = _backward_additional_bytes(plan, q, k, v)
+    room = budget - lean
+    if room > 0:
+        plan.ds_budget = room  # stores the tiles only if they fit in what is left
+        return _backward_additional_bytes(plan, q, k, v)
+    return lean
+
+
 def _preflight_backward(plan: _Plan, q, k, v) -> None:
-    _check_global_backward_budget(_backward_additional_bytes(plan, q, k, v), _free_hbm(q.device))
+    free = _free_hbm(q.device)
+    required = _fit_ds_budget(plan, q, k, v, _global_backward_budget(free))
+    _check_global_backward_budget(required, free)
+
+
+def _fit_local_backward(plan: _Plan, q, k, v) -> None:
+    # The local backward has no budget error in the reference (FA4's autograd
+    # allocates what it needs); its stored-dS band just shrinks to what fits.
+    _fit_ds_budget(plan, q, k, v, _global_backward_budget(_free_hbm(q.device)))
 
 
 def _preflight_forward_outputs(q: torch.Tensor) -> None:
@@ -769,6 +800,8 @@ def fa4_local_forward(
     ids = _prepare_vision_block_ids(vision_block_ids, q)
     plan = _fixed_plan(q, k, spec, vision=ids)
     _preflight_metadata_workspace(plan, q.device)
+    if _requires_backward(q, k, v):
+        _fit_local_backward(plan, q, k, v)
     return _run(q, k, v, plan)
 
 
@@ -804,6 +837,8 @@ def fa4_local_varlen_forward(
         )
         if vision is not None:
             _preflight_metadata_workspace(plan, q.device)
+        if _requires_backward(q, k, v):
+            _fit_local_backward(plan, q, k, v)
         return plan
 
     return _run_checked(q, k, v, check, prepare)

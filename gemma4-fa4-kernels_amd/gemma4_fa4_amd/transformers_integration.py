@@ -26,9 +26,18 @@ the native predicate (ti.py:543-647 states the same contract).  Two proofs:
    (``g4_mask_materialize``), for grids of at most ``_EVAL_PROOF_MAX_PAIRS``.
 
 Everything else fails closed with ``UnsupportedMI355XPath``.  The reference
-instead falls back to FlexAttention (ti.py:1607-1699), which on ROCm is a
-Triton kernel outside this library; ``allow_flex_fallback`` is accepted for
-signature compatibility and has no effect.
+instead falls back to FlexAttention for forward-only calls (ti.py:1607-1699,
+with a RuntimeWarning), which on ROCm is a Triton kernel outside this library;
+this build has one code path, the native one, so it behaves as the reference
+does with ``allow_flex_fallback=False`` (the same exception class, raised
+before any launch).  The argument is accepted for signature compatibility.
+
+The reference's budget fallback (ti.py:1950-1961: when the native global
+backward exceeds its HBM budget, re-run a low-memory composition) lives in the
+adapters here: the backward stores dS tiles only while they fit the budget and
+otherwise recomputes S and dP, so every caller gets it, and
+``GlobalBackwardBudgetExceeded`` is raised only when even that route does not
+fit.
 
 Padded query rows (2D padding mask) are returned as zeros with LSE ``-inf``,
 as the reference's unpacking does (ti.py:1418-1447).

@@ -331,3 +331,35 @@ def test_static_workspace_forward_rejects_a_problem_beyond_its_array():
                                 0x40000, lay, 0x50000, None)
     assert rc == _lib.G4_ERR_WORKSPACE
     assert b"static forward workspace" in lib.g4_last_error()
+
+
+def test_backward_budget_drops_stored_ds_before_failing(monkeypatch):
+    # The dS tiles are stored only while gradients + workspace fit the
+    # reference's budget (80% of free HBM, at most free - 2 GiB); past it the
+    # dQ stage recomputes (lean workspace); only when even that does not fit
+    # is GlobalBackwardBudgetExceeded raised (h100.py:713-746 policy).
+    s = 4096
+    q = torch.empty(s, 32, 512, dtype=torch.bfloat16)
+    k = torch.empty(s, 4, 512, dtype=torch.bfloat16)
+    v = torch.empty(s, 4, 512, dtype=torch.bfloat16)
+    cu = torch.tensor([0, s], dtype=torch.int32)
+    plan = att._packed_plan(q, k, cu, cu, s, s, g.GLOBAL_ATTENTION)
+    plan.ds_budget = 0
+    full = att._backward_additional_bytes(plan, q, k, v)
+    plan.ds_budget = -1
+    lean = att._backward_additional_bytes(plan, q, k, v)
+    assert full - lean == (s // 32 + 1) * 64 * 32 * 4096  # the stored dS tiles (packed rows)
+    gib = 1024 ** 3
+
+    def free_for(budget):  # free bytes whose budget is `budget`
+        return max(budget * 5 // 4 + 4, budget + 2 * gib)
+
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: free_for(full))
+    att._preflight_backward(plan, q, k, v)
+    assert plan.ds_budget == 0  # everything fits: default budget, tiles stored
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: free_for(full - 1))
+    att._preflight_backward(plan, q, k, v)
+    assert plan.ds_budget > 0 and att._backward_additional_bytes(plan, q, k, v) == lean
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: free_for(lean - 1))
+    with pytest.raises(g.GlobalBackwardBudgetExceeded):
+        att._preflight_backward(plan, q, k, v)
