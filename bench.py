@@ -216,12 +216,20 @@ def kv_prep_timing(torch, dev, reps: int):
 
     Source (1, 4, 8192, 512) bf16, fp32 cos / sin over 128 rotary dims (K in
     fp32, V in bf16) and bf16 tables (K and V in bf16, the attention's input).
-    Algorithmic bytes: forward reads Z, cos, sin, the weight and writes K, V;
-    backward reads Z, dK, dV, cos, sin, the weight and writes dZ (plus the
-    per-workgroup dweight partials, written and read once).
+    Kernel times: 20 back-to-back C-ABI launches between two HIP events on the
+    launch stream, per launch.  Per-call times: the autograd route
+    (prepare_global_kv_from_projection_source, torch.autograd.backward),
+    host work included.  Algorithmic bytes: forward reads Z, cos, sin, the
+    weight and writes K, V; backward reads Z, dK, dV, cos, sin, the weight and
+    writes dZ (plus the per-workgroup dweight partials, written and read once).
     """
-    import gemma4_fa4_amd as g
+    import ctypes
 
+    import gemma4_fa4_amd as g
+    from gemma4_fa4_amd import _lib
+    from gemma4_fa4_amd.kv_prep import _layout as kv_layout
+
+    lib = _lib.load()
     b, h, s, d, rot = 1, 4, 8192, 512, 128
     gen = torch.Generator(device=dev).manual_seed(7)
     z = torch.randn(b, h, s, d, generator=gen, device=dev).to(torch.bfloat16)
@@ -230,27 +238,55 @@ def kv_prep_timing(torch, dev, reps: int):
     out = {}
     for label, tdt in (("k_fp32", torch.float32), ("k_bf16", torch.bfloat16)):
         cos, sin = torch.cos(ang).to(tdt), torch.sin(ang).to(tdt)
+        c32, s32 = cos.float().contiguous(), sin.float().contiguous()
+        k_fp32 = tdt == torch.float32
+        kt = torch.empty(z.shape, dtype=torch.float32 if k_fp32 else torch.bfloat16, device=dev)
+        vt = torch.empty_like(z)
+        dk, dv = torch.randn_like(kt), torch.randn_like(vt)
+        dz, dw = torch.empty_like(z), torch.empty(d, dtype=torch.float32, device=dev)
+        prob = _lib.G4KvPrep(num_batches=b, seqlen=s, num_heads=h, head_dim=d, rotary_dim=rot,
+                             k_fp32=1 if k_fp32 else 0, eps=1e-6, cs_batch_stride=0)
+        ws = torch.empty(lib.g4_kv_prep_workspace_bytes(ctypes.byref(prob)), dtype=torch.uint8,
+                         device=dev)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        zl, kl, vl = kv_layout(z), kv_layout(kt), kv_layout(vt)
+
+        def fwd_launches(n=20):
+            for _ in range(n):
+                _lib.check(lib.g4_kv_prep_fwd(ctypes.byref(prob), z.data_ptr(), zl, w.data_ptr(),
+                                              c32.data_ptr(), s32.data_ptr(), kt.data_ptr(), kl,
+                                              vt.data_ptr(), vl, stream))
+
+        def bwd_launches(n=20):
+            for _ in range(n):
+                _lib.check(lib.g4_kv_prep_bwd(
+                    ctypes.byref(prob), z.data_ptr(), zl, w.data_ptr(), c32.data_ptr(),
+                    s32.data_ptr(), dk.data_ptr(), kl, dv.data_ptr(), vl, dz.data_ptr(), zl,
+                    dw.data_ptr(), ws.data_ptr(), ws.numel(), stream))
+
+        fwd_ms = statistics.median(event_times(torch, fwd_launches, 5, 1)) / 20
+        bwd_ms = statistics.median(event_times(torch, bwd_launches, 5, 1)) / 20
         zr = z.detach().requires_grad_(True)
         wr = w.detach().requires_grad_(True)
-        k, v = g.prepare_global_kv_from_projection_source(zr, k_norm_weight=wr, cos=cos, sin=sin)
-        dk, dv = torch.randn_like(k), torch.randn_like(v)
-        kb = k.element_size()
-        fwd_ms = statistics.median(event_times(torch, lambda: g.prepare_global_kv_from_projection_source(
+        kk, vv = g.prepare_global_kv_from_projection_source(zr, k_norm_weight=wr, cos=cos, sin=sin)
+        call_fwd = statistics.median(event_times(torch, lambda: g.prepare_global_kv_from_projection_source(
             z, k_norm_weight=w, cos=cos, sin=sin), reps, 2))
-        bwd_ms = statistics.median(event_times(
-            torch, lambda: torch.autograd.backward((k, v), (dk, dv), retain_graph=True), reps, 2))
+        call_bwd = statistics.median(event_times(
+            torch, lambda: torch.autograd.backward((kk, vv), (dk, dv), retain_graph=True), reps, 2))
         n = b * h * s * d
-        tables = 2 * b * s * rot * cos.element_size()
+        kb = kt.element_size()
+        tables = 2 * b * s * rot * 4
         fwd_bytes = n * 2 + tables + d * 4 + n * kb + n * 2
-        parts = min((b * h * s + 3) // 4, 2048) * d * 4
+        parts = min((b * h * s + 15) // 16, 512) * d * 4
         bwd_bytes = n * 2 + n * kb + n * 2 + tables + d * 4 + n * 2 + 2 * parts + d * 4
+        gbs = lambda nbytes, ms: round(nbytes / (ms * 1e-3) / 1e9, 1)  # noqa: E731
         out[label] = {
-            "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
-            "fwd_gbs": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9, 1),
-            "bwd_gbs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1),
-            "fwd_frac_hbm": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
-            "bwd_frac_hbm": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
+            "fwd_kernel_ms": round(fwd_ms, 4), "bwd_kernel_ms": round(bwd_ms, 4),
+            "fwd_gbs": gbs(fwd_bytes, fwd_ms), "bwd_gbs": gbs(bwd_bytes, bwd_ms),
+            "fwd_frac_hbm": round(gbs(fwd_bytes, fwd_ms) / PEAK_HBM_GBS, 3),
+            "bwd_frac_hbm": round(gbs(bwd_bytes, bwd_ms) / PEAK_HBM_GBS, 3),
             "fwd_bytes": fwd_bytes, "bwd_bytes": bwd_bytes,
+            "fwd_call_ms": round(call_fwd, 4), "bwd_call_ms": round(call_bwd, 4),
         }
     return out
 

@@ -28,7 +28,8 @@ namespace g4 {
 namespace {
 
 constexpr int kPrepD = 512;
-constexpr int kPrepWaves = 4;  // rows in flight per workgroup
+constexpr int kPrepWaves = 4;      // forward: rows in flight per workgroup
+constexpr int kPrepBwdWaves = 16;  // backward: more rows per dweight partial row
 
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
@@ -97,8 +98,12 @@ __global__ void __launch_bounds__(kPrepWaves * 64) kv_prep_fwd_kernel(
   }
   for (int64_t row = first; row < rows; row += step) {
     const RowAddr a = row_of(p, row);
-    float x[8];
+    float x[8], c[8], s[8];
     load8(z + elem_off(zl, a) + 8 * lane, x);
+    if (lane < rl) {  // issued with z, before the row reduction waits for it
+      load_rope(p, cosv, a, lane, c);
+      load_rope(p, sinv, a, lane, s);
+    }
     float ss = 0.f;
     {
 #pragma clang fp contract(off)
@@ -126,9 +131,6 @@ __global__ void __launch_bounds__(kPrepWaves * 64) kv_prep_fwd_kernel(
       // two rounded products and a rounded sum, as the reference's
       // x * cos + rotate_half(x) * sin (no fused multiply-add)
 #pragma clang fp contract(off)
-      float c[8], s[8];
-      load_rope(p, cosv, a, lane, c);
-      load_rope(p, sinv, a, lane, s);
       const float sign = lane < half ? -1.f : 1.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -164,15 +166,15 @@ __device__ __forceinline__ void load_dk(const g4_kv_prep& p, const void* dk, int
   }
 }
 
-__global__ void __launch_bounds__(kPrepWaves * 64) kv_prep_bwd_kernel(
+__global__ void __launch_bounds__(kPrepBwdWaves * 64) kv_prep_bwd_kernel(
     g4_kv_prep p, const __bf16* z, g4_layout zl, const float* w, const float* cosv,
     const float* sinv, const void* dk, g4_layout dkl, const __bf16* dv, g4_layout dvl,
     __bf16* dz, g4_layout dzl, float* dw_part, int64_t rows) {
-  __shared__ f32x4 red[kPrepWaves][64][2];
+  __shared__ f32x4 red[kPrepBwdWaves][64][2];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t first = (int64_t)blockIdx.x * kPrepWaves + wave;
-  const int64_t step = (int64_t)gridDim.x * kPrepWaves;
+  const int64_t first = (int64_t)blockIdx.x * kPrepBwdWaves + wave;
+  const int64_t step = (int64_t)gridDim.x * kPrepBwdWaves;
   const int rl = p.rotary_dim / 8;
   const int half = rl / 2;
   float wl[8], dwl[8];
@@ -187,26 +189,27 @@ __global__ void __launch_bounds__(kPrepWaves * 64) kv_prep_bwd_kernel(
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) dwl[e] = 0.f;
+  const int partner = lane < half ? lane + half : lane - half;
   for (int64_t row = first; row < rows; row += step) {
     const RowAddr a = row_of(p, row);
-    float x[8], gk[8], gv[8];
+    float x[8], gk[8], gv[8], c[8], ps[8];  // cos of this lane's dims, sin of the partner's
     load8(z + elem_off(zl, a) + 8 * lane, x);
     load_dk(p, dk, elem_off(dkl, a) + 8 * lane, gk);
     load8(dv + elem_off(dvl, a) + 8 * lane, gv);
+    if (lane < rl) {
+      load_rope(p, cosv, a, lane, c);
+      load_rope(p, sinv, a, partner, ps);
+    }
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
     ss = wave_sum(ss);
     const float r = 1.f / __fsqrt_rn(ss / (float)kPrepD + p.eps);
     // adjoint of the RoPE: the partner lane's dK times its sin
-    const int partner = lane < half ? lane + half : lane - half;
     float pg[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) pg[e] = __shfl(gk[e], partner, 64);
     if (lane < rl) {
-      float c[8], ps[8];  // cos of this lane's dims, sin of the partner's
-      load_rope(p, cosv, a, lane, c);
-      load_rope(p, sinv, a, partner, ps);
       const float sign = lane < half ? 1.f : -1.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) gk[e] = gk[e] * c[e] + sign * pg[e] * ps[e];
@@ -233,7 +236,7 @@ __global__ void __launch_bounds__(kPrepWaves * 64) kv_prep_bwd_kernel(
   if (wave == 0) {
     f32x4 s0 = red[0][lane][0], s1 = red[0][lane][1];
 #pragma unroll
-    for (int wv = 1; wv < kPrepWaves; ++wv) {
+    for (int wv = 1; wv < kPrepBwdWaves; ++wv) {
       s0 += red[wv][lane][0];
       s1 += red[wv][lane][1];
     }
@@ -243,21 +246,33 @@ __global__ void __launch_bounds__(kPrepWaves * 64) kv_prep_bwd_kernel(
   }
 }
 
-// dw[d] = sum over workgroups b (in order) of dw_part[b][d].
+// dw[d] = sum over workgroups of dw_part[b][d] in a fixed order: a block owns
+// 8 columns; thread (g, c) sums rows b = g, g + 32, ... of column c in order,
+// then thread g = 0 adds the 32 group sums in group order.
 __global__ void __launch_bounds__(256) kv_prep_dw_kernel(const float* dw_part, int nparts,
                                                          float* dw) {
-  const int d = blockIdx.x * blockDim.x + threadIdx.x;
-  if (d >= kPrepD) return;
+  __shared__ float part[32][8];
+  const int c = threadIdx.x & 7, g = threadIdx.x >> 3;
+  const int d = blockIdx.x * 8 + c;
   float s = 0.f;
-  for (int b = 0; b < nparts; ++b) s += dw_part[(int64_t)b * kPrepD + d];
-  dw[d] = s;
+  for (int b = g; b < nparts; b += 32) s += dw_part[(int64_t)b * kPrepD + d];
+  part[g][c] = s;
+  __syncthreads();
+  if (g == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) t += part[i][c];
+    dw[d] = t;
+  }
 }
 
 }  // namespace
 
+// Workgroups of the backward (each writes one row of dweight partials):
+// enough waves to keep HBM busy, few partial rows to sum.
 int kv_prep_blocks(int64_t rows) {
-  const int64_t want = (rows + kPrepWaves - 1) / kPrepWaves;
-  return (int)std::min<int64_t>(want, 2048);
+  const int64_t want = (rows + kPrepBwdWaves - 1) / kPrepBwdWaves;
+  return (int)std::min<int64_t>(want, 512);
 }
 
 size_t kv_prep_workspace_bytes(const g4_kv_prep& p) {
@@ -270,7 +285,8 @@ hipError_t launch_kv_prep_fwd(const g4_kv_prep& p, const void* z, g4_layout zl, 
                               void* v, g4_layout vl, hipStream_t stream) {
   const int64_t rows = (int64_t)p.num_batches * p.seqlen * p.num_heads;
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(kv_prep_fwd_kernel, dim3(kv_prep_blocks(rows)), dim3(kPrepWaves * 64), 0,
+  const int fwd_blocks = (int)std::min<int64_t>((rows + kPrepWaves - 1) / kPrepWaves, 4096);
+  hipLaunchKernelGGL(kv_prep_fwd_kernel, dim3(fwd_blocks), dim3(kPrepWaves * 64), 0,
                      stream, p, (const __bf16*)z, zl, w, cosv, sinv, k, kl, (__bf16*)v, vl, rows);
   return hipGetLastError();
 }
@@ -282,13 +298,13 @@ hipError_t launch_kv_prep_bwd(const g4_kv_prep& p, const void* z, g4_layout zl, 
   const int64_t rows = (int64_t)p.num_batches * p.seqlen * p.num_heads;
   const int blocks = rows > 0 ? kv_prep_blocks(rows) : 0;
   if (blocks > 0) {
-    hipLaunchKernelGGL(kv_prep_bwd_kernel, dim3(blocks), dim3(kPrepWaves * 64), 0, stream, p,
+    hipLaunchKernelGGL(kv_prep_bwd_kernel, dim3(blocks), dim3(kPrepBwdWaves * 64), 0, stream, p,
                        (const __bf16*)z, zl, w, cosv, sinv, dk, dkl, (const __bf16*)dv, dvl,
                        (__bf16*)dz, dzl, (float*)ws, rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(kv_prep_dw_kernel, dim3((kPrepD + 255) / 256), dim3(256), 0, stream,
+  hipLaunchKernelGGL(kv_prep_dw_kernel, dim3(kPrepD / 8), dim3(256), 0, stream,
                      (const float*)ws, blocks, dw);
   return hipGetLastError();
 }
