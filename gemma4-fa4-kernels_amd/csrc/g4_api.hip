@@ -402,8 +402,8 @@ static int check_kv_prep(const g4_kv_prep* p) {
   if (p == nullptr) return fail(G4_ERR_INVALID, "K/V preparation descriptor is NULL");
   if (p->num_batches < 1 || p->seqlen < 1 || p->num_heads < 1)
     return fail(G4_ERR_INVALID, "num_batches, seqlen and num_heads must be >= 1");
-  if (p->head_dim != 512)
-    return fail(G4_ERR_UNSUPPORTED, "K/V preparation supports head_dim 512 (the global layer)");
+  if (p->head_dim != 512 && p->head_dim != 256)
+    return fail(G4_ERR_UNSUPPORTED, "K/V preparation supports head_dim 512 and 256");
   if (p->rotary_dim < 0 || p->rotary_dim > p->head_dim || p->rotary_dim % 16)
     return fail(G4_ERR_INVALID, "rotary_dim must be a multiple of 16 in [0, head_dim]");
   if (!(p->eps >= 0.f) || p->eps > 1.f) return fail(G4_ERR_INVALID, "eps must be in [0, 1]");
@@ -422,10 +422,11 @@ static int check_prep_operand(const void* ptr, const g4_layout& l, const char* n
   return G4_OK;
 }
 
-static int check_prep_tables(const g4_kv_prep* p, const float* w, const float* c, const float* s) {
+static int check_prep_tables(const g4_kv_prep* p, const float* w, const float* c, const float* s,
+                             bool rope = true) {
   if (w == nullptr || ((uintptr_t)w) % 16)
     return fail(G4_ERR_INVALID, "weight must be a 16-byte aligned fp32 array");
-  if (p->rotary_dim > 0 && (c == nullptr || s == nullptr || ((uintptr_t)c) % 16 ||
+  if (rope && p->rotary_dim > 0 && (c == nullptr || s == nullptr || ((uintptr_t)c) % 16 ||
                             ((uintptr_t)s) % 16))
     return fail(G4_ERR_INVALID, "cos and sin must be 16-byte aligned fp32 arrays");
   return G4_OK;
@@ -437,9 +438,11 @@ int g4_kv_prep_fwd(const g4_kv_prep* p, const void* z, g4_layout zl, const float
   g_last_error.clear();
   G4_TRY(check_kv_prep(p));
   G4_TRY(check_prep_operand(z, zl, "z"));
-  G4_TRY(check_prep_operand(k, kl, "k"));
-  G4_TRY(check_prep_operand(v, vl, "v"));
-  G4_TRY(check_prep_tables(p, weight, cosv, sinv));
+  if (k == nullptr && v == nullptr) return fail(G4_ERR_INVALID, "both K and V are NULL");
+  if (k != nullptr) G4_TRY(check_prep_operand(k, kl, "k"));
+  if (v != nullptr) G4_TRY(check_prep_operand(v, vl, "v"));
+  G4_TRY(check_prep_tables(p, weight, k != nullptr ? cosv : nullptr, k != nullptr ? sinv : nullptr,
+                           k != nullptr));
   hipError_t e = g4::launch_kv_prep_fwd(*p, z, zl, weight, cosv, sinv, k, kl, v, vl,
                                         (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "K/V preparation forward");
@@ -458,6 +461,8 @@ int g4_kv_prep_bwd(const g4_kv_prep* p, const void* z, g4_layout zl, const float
                    void* ws, size_t ws_bytes, void* stream) {
   g_last_error.clear();
   G4_TRY(check_kv_prep(p));
+  if (p->head_dim != 512)
+    return fail(G4_ERR_UNSUPPORTED, "the K/V preparation backward covers head_dim 512");
   G4_TRY(check_prep_operand(z, zl, "z"));
   G4_TRY(check_prep_operand(dk, dkl, "dk"));
   G4_TRY(check_prep_operand(dv, dvl, "dv"));

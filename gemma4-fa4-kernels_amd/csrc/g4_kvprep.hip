@@ -1,18 +1,22 @@
-// Global-layer K/V preparation from the shared projection source, fused.
+// K/V (and Q) preparation from a projection source, fused.
 //
-// Per (token, KV head) row z of head_dim = 512:
+// Per (token, head) row z of head_dim D (512 for the global layer's shared
+// K/V source and its queries, 256 for the sliding layers' queries and keys):
 //   r  = (mean(z^2) + eps)^(-1/2)            (fp32 over the row)
 //   n  = z r                                  (fp32)
 //   V  = bf16(n)                              (RMSNorm without a weight)
 //   kn = bf16(n w)                            (RMSNorm with the learned weight)
 //   K  = kn with RoPE on its first R dims: K_i = kn_i cos_i + rot(kn)_i sin_i,
-//        rot(x)_i = -x_{i+R/2} (i < R/2), x_{i-R/2} (R/2 <= i < R), fp32 products
-//        and sum, no contraction; the other dims pass through.
-// One wave per row, lane l holding dims 8l .. 8l + 7 (one 16-byte load), so the
-// row reduction is a wave reduction and rot(x) is a lane exchange with lane
-// l +- R/16.  HBM-bound: each row reads 1 KB of z and writes K and V.
+//        rot(x)_i = -x_{i+R/2} (i < R/2), x_{i-R/2} (R/2 <= i < R); the other
+//        dims pass through.  K in fp32 (fp32 tables): fp32 products and sum,
+//        no contraction.  K in bf16 (bf16 tables): each product and the sum
+//        rounded to bf16, as bf16 tensor operations round them.
+// One wave per row, lane l holding dims E l .. E l + E - 1 (E = D / 64: one
+// 16- or 8-byte load), so the row reduction is a wave reduction and rot(x) is
+// a lane exchange with lane l +- R / (2 E).  HBM-bound: each row reads 2 D
+// bytes of z and writes K and V (either may be left out).
 //
-// Backward (fp32 throughout, dz rounded to bf16 once):
+// Backward (D = 512; fp32 throughout, dz rounded to bf16 once):
 //   g_k  = adjoint of the RoPE applied to dK: i < R/2: dK_i cos_i + dK_{i+R/2} sin_{i+R/2};
 //          R/2 <= i < R: dK_i cos_i - dK_{i-R/2} sin_{i-R/2}; pass dims dK_i
 //   g_n  = g_k w + dV,   dw += g_k n  (summed over every row)
@@ -78,73 +82,104 @@ __device__ __forceinline__ void load_rope(const g4_kv_prep& p, const float* cs, 
   }
 }
 
+template <int E>
+using bf16v = __bf16 __attribute__((ext_vector_type(E)));
+
+// E consecutive bf16 / fp32 elements of this lane.
+template <int E>
+__device__ __forceinline__ void load_e(const __bf16* p, float (&x)[E]) {
+  const bf16v<E> v = *(const bf16v<E>*)p;
+#pragma unroll
+  for (int e = 0; e < E; ++e) x[e] = (float)v[e];
+}
+
+template <int E>
+__device__ __forceinline__ void store_e(__bf16* p, const float (&x)[E]) {
+  bf16v<E> v;
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = (__bf16)x[e];
+  *(bf16v<E>*)p = v;
+}
+
+template <int E>
+__device__ __forceinline__ void load_e(const float* p, float (&x)[E]) {
+#pragma unroll
+  for (int j = 0; j < E / 4; ++j) {
+    const f32x4 v = *(const f32x4*)(p + 4 * j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[4 * j + e] = v[e];
+  }
+}
+
+template <int E>
 __global__ void __launch_bounds__(kPrepWaves * 64) kv_prep_fwd_kernel(
     g4_kv_prep p, const __bf16* z, g4_layout zl, const float* w, const float* cosv,
     const float* sinv, void* k, g4_layout kl, __bf16* v, g4_layout vl, int64_t rows) {
+  constexpr int D = 64 * E;
   const int lane = threadIdx.x & 63;
   const int64_t first = (int64_t)blockIdx.x * kPrepWaves + (threadIdx.x >> 6);
   const int64_t step = (int64_t)gridDim.x * kPrepWaves;
-  const int rl = p.rotary_dim / 8;  // lanes holding rotary dims
+  const int rl = p.rotary_dim / E;  // lanes holding rotary dims
   const int half = rl / 2;          // lane distance of the rotate-half partner
-  float wl[8];
-  {
-    const f32x4 lo = *(const f32x4*)(w + 8 * lane);
-    const f32x4 hi = *(const f32x4*)(w + 8 * lane + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      wl[e] = lo[e];
-      wl[4 + e] = hi[e];
-    }
-  }
+  float wl[E];
+  load_e<E>(w + E * lane, wl);
   for (int64_t row = first; row < rows; row += step) {
     const RowAddr a = row_of(p, row);
-    float x[8], c[8], s[8];
-    load8(z + elem_off(zl, a) + 8 * lane, x);
-    if (lane < rl) {  // issued with z, before the row reduction waits for it
-      load_rope(p, cosv, a, lane, c);
-      load_rope(p, sinv, a, lane, s);
+    float x[E], c[E], s[E];
+    load_e<E>(z + elem_off(zl, a) + E * lane, x);
+    if (k != nullptr && lane < rl) {  // issued with z, before the row reduction waits for it
+      const int64_t t = a.b * p.cs_batch_stride + a.t * (int64_t)p.rotary_dim + E * lane;
+      load_e<E>(cosv + t, c);
+      load_e<E>(sinv + t, s);
     }
     float ss = 0.f;
     {
 #pragma clang fp contract(off)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];  // rounded squares, then sums
+      for (int e = 0; e < E; ++e) ss += x[e] * x[e];  // rounded squares, then sums
     }
     ss = wave_sum(ss);
-    const float r = 1.f / __fsqrt_rn(ss / (float)kPrepD + p.eps);
-    float n[8], kn[8];
+    const float r = 1.f / __fsqrt_rn(ss / (float)D + p.eps);
+    float n[E], kn[E];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < E; ++e) {
       n[e] = x[e] * r;
       kn[e] = (float)(__bf16)(n[e] * wl[e]);
     }
-    store8(v + elem_off(vl, a) + 8 * lane, n);
+    if (v != nullptr) store_e<E>(v + elem_off(vl, a) + E * lane, n);
+    if (k == nullptr) continue;
     // rotate-half partner values (every lane takes part in the exchange)
     const int partner = lane < half ? lane + half : lane - half;
-    float pk[8];
+    float pk[E];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) pk[e] = __shfl(kn[e], partner, 64);
-    float kout[8];
+    for (int e = 0; e < E; ++e) pk[e] = __shfl(kn[e], partner, 64);
+    float kout[E];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) kout[e] = kn[e];
+    for (int e = 0; e < E; ++e) kout[e] = kn[e];
     if (lane < rl) {
-      // two rounded products and a rounded sum, as the reference's
-      // x * cos + rotate_half(x) * sin (no fused multiply-add)
+      // x * cos + rotate_half(x) * sin as two products and a sum, no fused
+      // multiply-add; in bf16 each product is rounded before the sum (the
+      // products of bf16 values are exact in fp32, so one rounding each)
 #pragma clang fp contract(off)
       const float sign = lane < half ? -1.f : 1.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float a0 = kn[e] * c[e];
-        const float a1 = (sign * pk[e]) * s[e];
+      for (int e = 0; e < E; ++e) {
+        float a0 = kn[e] * c[e];
+        float a1 = (sign * pk[e]) * s[e];
+        if (!p.k_fp32) {
+          a0 = (float)(__bf16)a0;
+          a1 = (float)(__bf16)a1;
+        }
         kout[e] = a0 + a1;
       }
     }
     if (p.k_fp32) {
-      float* kp = (float*)k + elem_off(kl, a) + 8 * lane;
-      *(f32x4*)kp = f32x4{kout[0], kout[1], kout[2], kout[3]};
-      *(f32x4*)(kp + 4) = f32x4{kout[4], kout[5], kout[6], kout[7]};
+      float* kp = (float*)k + elem_off(kl, a) + E * lane;
+#pragma unroll
+      for (int j = 0; j < E / 4; ++j)
+        *(f32x4*)(kp + 4 * j) = f32x4{kout[4 * j], kout[4 * j + 1], kout[4 * j + 2], kout[4 * j + 3]};
     } else {
-      store8((__bf16*)k + elem_off(kl, a) + 8 * lane, kout);
+      store_e<E>((__bf16*)k + elem_off(kl, a) + E * lane, kout);
     }
   }
 }
@@ -286,8 +321,14 @@ hipError_t launch_kv_prep_fwd(const g4_kv_prep& p, const void* z, g4_layout zl, 
   const int64_t rows = (int64_t)p.num_batches * p.seqlen * p.num_heads;
   if (rows <= 0) return hipSuccess;
   const int fwd_blocks = (int)std::min<int64_t>((rows + kPrepWaves - 1) / kPrepWaves, 4096);
-  hipLaunchKernelGGL(kv_prep_fwd_kernel, dim3(fwd_blocks), dim3(kPrepWaves * 64), 0,
-                     stream, p, (const __bf16*)z, zl, w, cosv, sinv, k, kl, (__bf16*)v, vl, rows);
+  if (p.head_dim == 256)
+    hipLaunchKernelGGL(kv_prep_fwd_kernel<4>, dim3(fwd_blocks), dim3(kPrepWaves * 64), 0,
+                       stream, p, (const __bf16*)z, zl, w, cosv, sinv, k, kl, (__bf16*)v, vl,
+                       rows);
+  else
+    hipLaunchKernelGGL(kv_prep_fwd_kernel<8>, dim3(fwd_blocks), dim3(kPrepWaves * 64), 0,
+                       stream, p, (const __bf16*)z, zl, w, cosv, sinv, k, kl, (__bf16*)v, vl,
+                       rows);
   return hipGetLastError();
 }
 

@@ -15,7 +15,22 @@ from .attention import (
     fa4_local_text_forward,
     fa4_local_varlen_forward,
 )
+from . import torch_ops
 from .errors import GlobalBackwardBudgetExceeded, UnsupportedH100Path, UnsupportedMI355XPath
+from .facades import (
+    Gemma4H100CompiledLayerFacade,
+    Gemma4H100CompiledLocalStaticCacheDecodeFacade,
+    Gemma4H100CompiledStaticCacheDecodeFacade,
+    Gemma4MI355XCompiledLayerFacade,
+    Gemma4MI355XCompiledLocalStaticCacheDecodeFacade,
+    Gemma4MI355XCompiledStaticCacheDecodeFacade,
+    compile_gemma4_fa4_h100_layer,
+    compile_gemma4_fa4_h100_static_cache_decode,
+    compile_gemma4_mi355x_layer,
+    compile_gemma4_mi355x_static_cache_decode,
+    gemma4_fa4_compile_layer,
+    gemma4_mi355x_compile_layer,
+)
 from .kv_prep import prepare_global_kv_from_projection_source
 from .model_spec import (
     GEMMA4_31B,
@@ -60,4 +75,17 @@ __all__ = [
     "gemma4_fa4_prepared",
     "register_gemma4_fa4_h100",
     "register_gemma4_mi355x",
+    "torch_ops",
+    "Gemma4MI355XCompiledLayerFacade",
+    "Gemma4MI355XCompiledStaticCacheDecodeFacade",
+    "Gemma4MI355XCompiledLocalStaticCacheDecodeFacade",
+    "Gemma4H100CompiledLayerFacade",
+    "Gemma4H100CompiledStaticCacheDecodeFacade",
+    "Gemma4H100CompiledLocalStaticCacheDecodeFacade",
+    "compile_gemma4_mi355x_layer",
+    "compile_gemma4_mi355x_static_cache_decode",
+    "compile_gemma4_fa4_h100_layer",
+    "compile_gemma4_fa4_h100_static_cache_decode",
+    "gemma4_mi355x_compile_layer",
+    "gemma4_fa4_compile_layer",
 ]

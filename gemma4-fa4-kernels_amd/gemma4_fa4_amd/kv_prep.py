@@ -14,9 +14,15 @@ Same signature and result dtypes as the reference: the source is
 ``(B, S, R)`` or ``(S, R)`` with ``R = D * partial_rotary_factor``; V has the
 source's dtype and K the promoted dtype of source and cos / sin (fp32 for the
 usual bf16 source with fp32 tables).  The kernel computes the RMSNorm in fp32
-and the rotation in fp32 (two rounded products and a rounded sum, as the
-reference's fp32 operations); bf16 tables are widened to fp32, so K is then
-rounded once where the reference's bf16 operations round three times.
+and the rotation in K's dtype the way the reference's tensor operations do:
+with fp32 tables two rounded fp32 products and a rounded sum, with bf16 tables
+each product and the sum rounded to bf16.
+
+``prepare_rows_into`` is the same kernel without autograd, for the inference
+boundaries (the compiled layer and StaticCache decode operators): it writes
+the RMSNorm + RoPE of query or key rows, and the unweighted RMSNorm of value
+rows, of head_dim 512 or 256 straight into caller-provided views (a cache
+slot, a BSHD buffer seen as BHSD).
 """
 
 from __future__ import annotations
@@ -151,3 +157,74 @@ def prepare_global_kv_from_projection_source(
     if k_dtype not in (torch.bfloat16, torch.float32):
         raise UnsupportedMI355XPath("K is produced as BF16 or FP32 (cos / sin in BF16 or FP32)")
     return _KvPrepFunction.apply(source, k_norm_weight, cos, sin, rot, eps, k_dtype)
+
+
+def prepare_rows_into(
+    source: torch.Tensor,
+    *,
+    weight: torch.Tensor,
+    cos: torch.Tensor | None = None,
+    sin: torch.Tensor | None = None,
+    rotary_dim: int = 0,
+    eps: float = 1e-6,
+    k: torch.Tensor | None = None,
+    v: torch.Tensor | None = None,
+) -> None:
+    """Inference-only preparation of (B, H, S, D) rows into the views ``k`` / ``v``.
+
+    ``k`` receives RoPE(RMSNorm(source) * weight) over the first ``rotary_dim``
+    dims (bf16 with bf16 tables, fp32 with fp32 tables), ``v`` the unweighted
+    RMSNorm (bf16); either may be None.  Every tensor is (B, H, S, D) with a
+    unit last-dim stride (views of BSHD buffers and of cache slots included);
+    no gradients are produced.
+    """
+    if k is None and v is None:
+        raise ValueError("at least one of k and v must be given")
+    if source.ndim != 4 or source.dtype != torch.bfloat16:
+        raise ValueError("the projection source must be a rank-4 BF16 (B, H, S, D) tensor")
+    if source.device.type != "cuda":
+        raise UnsupportedMI355XPath("the MI355X K/V preparation needs GPU tensors")
+    d = source.shape[-1]
+    if d not in (256, 512):
+        raise UnsupportedMI355XPath("the MI355X row preparation covers head_dim 512 and 256")
+    if rotary_dim < 0 or rotary_dim > d or rotary_dim % 16:
+        raise ValueError("rotary_dim must be a multiple of 16 in [0, head_dim]")
+    if weight.shape != (d,):
+        raise ValueError("the norm weight must have shape (head_dim,)")
+    for name, t in (("source", source), ("k", k), ("v", v)):
+        if t is None:
+            continue
+        if t.shape != source.shape or t.device != source.device:
+            raise ValueError(f"{name} must match the source's shape and device")
+        if t.stride(-1) != 1 or any(s <= 0 or s % 8 for s in t.stride()[:-1]) or \
+                t.data_ptr() % 16:
+            raise ValueError(f"{name} needs a unit last-dim stride, positive outer strides "
+                             "that are multiples of 8 and a 16-byte aligned base")
+    if v is not None and v.dtype != torch.bfloat16:
+        raise ValueError("v is written as BF16")
+    b, _, s, _ = source.shape
+    c = sn = None
+    stride = 0
+    k_fp32 = False
+    if k is not None:
+        if k.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError("k is written as BF16 or FP32")
+        k_fp32 = k.dtype == torch.float32
+        if rotary_dim:
+            if cos is None or sin is None:
+                raise ValueError("cos and sin are required for a rotary k")
+            table_dtype = torch.promote_types(cos.dtype, sin.dtype)
+            if torch.promote_types(source.dtype, table_dtype) != k.dtype:
+                raise ValueError("k's dtype must be the promoted dtype of source, cos and sin")
+            c, sn, stride = _tables(cos, sin, b, s, rotary_dim)
+    w = weight.to(torch.float32).contiguous()
+    lib = _lib.load()
+    prob = _problem(source, rotary_dim, eps, stride, k_fp32)
+    null = G4Layout(0, 0, 0)
+    with torch.cuda.device(source.device):
+        _lib.check(lib.g4_kv_prep_fwd(
+            ctypes.byref(prob), source.data_ptr(), _layout(source), w.data_ptr(),
+            c.data_ptr() if c is not None else None, sn.data_ptr() if sn is not None else None,
+            k.data_ptr() if k is not None else None, _layout(k) if k is not None else null,
+            v.data_ptr() if v is not None else None, _layout(v) if v is not None else null,
+            _stream(source.device)))

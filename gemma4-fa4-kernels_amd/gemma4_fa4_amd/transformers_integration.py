@@ -41,6 +41,15 @@ fit.
 
 Padded query rows (2D padding mask) are returned as zeros with LSE ``-inf``,
 as the reference's unpacking does (ti.py:1418-1447).
+
+Under ``torch.compile`` or with FakeTensor inputs, a text-only single
+sequence (B = 1, S <= 1024, the layer's causal / sliding-causal mask, explicit
+position_ids) is routed to one opaque custom operator of ``torch_ops``
+(ti.py:761-921); everything else fails closed there.  The reference further
+requires the exact pinned Transformers ``Gemma4TextAttention`` class and its
+own compile-origin mask markers, which belong to a Transformers revision that
+is not installed here; this route checks the mask callable structurally
+instead.
 """
 
 from __future__ import annotations
@@ -660,6 +669,115 @@ def _packed_metadata(values, seg, all_valid):
 # --------------------------------------------------------------------------
 
 
+# --------------------------------------------------------------------------
+# torch.compile / FakeTensor route (ti.py:761-921)
+# --------------------------------------------------------------------------
+
+
+def _is_fake(t: torch.Tensor) -> bool:
+    try:
+        from torch._subclasses.fake_tensor import FakeTensor
+    except ImportError:  # pragma: no cover
+        return False
+    return isinstance(t, FakeTensor)
+
+
+def _compiling() -> bool:
+    compiler = getattr(torch, "compiler", None)
+    is_compiling = getattr(compiler, "is_compiling", None)
+    return bool(is_compiling()) if callable(is_compiling) else False
+
+
+def _compiled_forward(module, query, key, value, plan, spec: AttentionLayerSpec, *,
+                      position_ids, vision_block_ids, document_ids, cu_seq_lens_q,
+                      cu_seq_lens_k, max_length_q, max_length_k, extra) -> Gemma4DispatchResult:
+    """Admit one text sequence as a single opaque custom operator.
+
+    The reference's compiled fixed-forward ABI (ti.py:761-921): an eval-mode
+    module, a mask plan without padding or offsets whose mask is the text-only
+    predicate of the layer (causal; causal within the window for sliding
+    layers), B = 1, Sq = Sk in 1..1024, BF16 prepared q/k/v of the locked
+    geometry, explicit position_ids, and no metadata, packed lengths or cache.
+    The operator (``gemma4_mi355x::local_fwd`` / ``global_fwd``) is opaque to
+    the tracer and checks positions on the device when it runs.
+    """
+    label = "FakeTensor/torch.compile"
+    if getattr(module, "training", False):
+        raise UnsupportedMI355XPath(f"{label} routing requires an eval-mode attention module")
+    if not isinstance(plan, Gemma4MaskPlan):
+        raise UnsupportedMI355XPath(f"Transformers {label} requires a Gemma4MaskPlan")
+    if plan.attention_mask is not None:
+        raise UnsupportedMI355XPath(f"{label} does not accept padding or explicit masks")
+    for name in ("q_offset", "kv_offset"):
+        offset = getattr(plan, name)
+        if type(offset) is not int or offset != 0:
+            raise UnsupportedMI355XPath(f"{label} does not accept {name.split('_')[0].upper()} "
+                                        "offsets")
+    if plan.mask_function is not None and getattr(plan, "_g4_origin", None) is not _NATIVE_ORIGIN:
+        mu = _masking_utils()
+        rec = _Recognizer(mu) if mu is not None else None
+        term = rec.term(plan.mask_function) if rec is not None else None
+        if term is None or rec.captured["vision"] or rec.captured["packed"] or \
+                term != _expected_term(spec, vision=False, packed=False):
+            raise UnsupportedMI355XPath(f"{label} accepts only the layer's text-only mask "
+                                        "(causal, or causal within the sliding window)")
+    tensors = (query, key, value)
+    if any(t.ndim != 4 for t in tensors):
+        raise UnsupportedMI355XPath(f"{label} requires rank-4 prepared BHSD Q/K/V")
+    if not (query.device == key.device == value.device) or query.device.type != "cuda":
+        raise UnsupportedMI355XPath(f"{label} requires Q/K/V on one CUDA device")
+    if any(t.dtype != torch.bfloat16 for t in tensors):
+        raise UnsupportedMI355XPath(f"{label} requires BF16 prepared Q/K/V")
+    if not _compiling():
+        fake = [_is_fake(t) for t in tensors]
+        if any(fake) and not all(fake):
+            raise UnsupportedMI355XPath(f"{label} requires Q/K/V to share one tensor mode")
+    if any(t.requires_grad for t in tensors):
+        raise UnsupportedMI355XPath(f"{label} is forward-only and rejects requires_grad inputs")
+    b, hq, sq, dq = query.shape
+    kb, hkv, sk, dk = key.shape
+    if b != 1 or kb != 1 or value.shape[0] != 1:
+        raise UnsupportedMI355XPath(f"{label} accepts B1 only")
+    if sq != sk or value.shape[2] != sk:
+        raise UnsupportedMI355XPath(f"{label} requires equal Q/K/V sequence lengths")
+    if not 1 <= sq <= 1024:
+        raise UnsupportedMI355XPath(f"{label} requires a sequence length in 1..1024")
+    if (hq, dq) != (spec.num_q_heads, spec.head_dim_qk):
+        raise UnsupportedMI355XPath(f"{label} Q geometry conflicts with the locked layer")
+    if (hkv, dk) != (spec.num_kv_heads, spec.head_dim_qk) or \
+            tuple(value.shape[1:]) != (spec.num_kv_heads, sk, spec.head_dim_v):
+        raise UnsupportedMI355XPath(f"{label} K/V geometry conflicts with the locked layer")
+    if (plan.batch_size, plan.q_length, plan.kv_length) != (b, sq, sk):
+        raise UnsupportedMI355XPath("mask plan dimensions do not match prepared Q/K/V")
+    if not isinstance(position_ids, torch.Tensor):
+        raise UnsupportedMI355XPath(f"{label} requires explicit position_ids")
+    if position_ids.ndim != 2 or tuple(position_ids.shape) != (1, sq) or \
+            position_ids.device != query.device or \
+            position_ids.dtype not in (torch.int32, torch.int64):
+        raise UnsupportedMI355XPath("compiled position_ids must be CUDA INT32/INT64 with shape "
+                                    "(1, S)")
+    if vision_block_ids is not None or document_ids is not None:
+        raise UnsupportedMI355XPath(f"{label} accepts text-only requests without metadata")
+    if any(x is not None for x in (cu_seq_lens_q, cu_seq_lens_k, max_length_q, max_length_k)):
+        raise UnsupportedMI355XPath(f"{label} does not accept packed sequence metadata")
+    if any(extra.get(name) is not None for name in ("past_key_values", "cache",
+                                                    "cache_position")):
+        raise UnsupportedMI355XPath(f"{label} does not accept a cache")
+    from . import torch_ops
+
+    if not torch_ops.CUSTOM_OPS_AVAILABLE:  # pragma: no cover
+        raise UnsupportedMI355XPath(f"{label} requires torch.library custom_op and register_fake")
+    # packed-sequence ids implied by the positions: a new run wherever the
+    # position does not advance by one (the operator checks them on the device)
+    first = position_ids[:, :1] - 1
+    packed = (torch.diff(position_ids, prepend=first, dim=-1) != 1).cumsum(-1)
+    if spec.kind == "full_attention":
+        out, lse = torch_ops.global_fwd(query, key, value, position_ids, packed)
+        return Gemma4DispatchResult(out, lse, "fa4_global_compiled_op")
+    out, lse = torch_ops.local_fwd(query, key, value, position_ids, packed)
+    return Gemma4DispatchResult(out, lse, "fa4_local_compiled_op")
+
+
 def gemma4_fa4_prepared(
     module: Any,
     query: torch.Tensor,
@@ -688,6 +806,13 @@ def gemma4_fa4_prepared(
         module, spec, dropout=dropout, scaling=scaling, sliding_window=sliding_window,
         output_attentions=output_attentions,
     )
+    if _compiling() or any(_is_fake(t) for t in (query, key, value)):
+        return _compiled_forward(
+            module, query, key, value, attention_mask, spec, position_ids=position_ids,
+            vision_block_ids=vision_block_ids, document_ids=document_ids,
+            cu_seq_lens_q=cu_seq_lens_q, cu_seq_lens_k=cu_seq_lens_k,
+            max_length_q=max_length_q, max_length_k=max_length_k, extra=_kwargs,
+        )
     B, Sq, Sk = _validate_prepared(query, key, value, spec)
     device = query.device
     local = spec.kind != "full_attention"

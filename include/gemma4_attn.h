@@ -221,23 +221,26 @@ int g4_tile_ranges(const g4_problem* p, int direction, int row_tile, int32_t* ou
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Global-layer K/V preparation from the shared projection source (the
- * reference's prepare_global_kv_from_projection_source,
- * src/gemma4_fa4/reference.py:306-328, with rms_norm 276-281 and partial
- * RoPE 284-303; design note docs/design.md:202-213).  Per (batch, token,
- * head) row z of head_dim elements:
+ * K/V preparation from a projection source (the reference's
+ * prepare_global_kv_from_projection_source, src/gemma4_fa4/reference.py:306-328,
+ * with rms_norm 276-281 and partial RoPE 284-303; design note
+ * docs/design.md:202-213; the same RMSNorm and RoPE order as the compiled
+ * layer ops' _rms_norm / _apply_rotary, src/gemma4_fa4/h100_torch_ops.py:302-326).
+ * Per (batch, token, head) row z of head_dim elements:
  *   r = (mean(z^2) + eps)^(-1/2), n = z r               (fp32)
  *   V = bf16(n)                                          (RMSNorm, no weight)
  *   kn = bf16(n w); K = kn with RoPE on its first rotary_dim dims
  *        (K_i = kn_i cos_i + rot(kn)_i sin_i, rot(x) = (-x2, x1) over the
- *        rotary dims, fp32 products and sum), other dims unchanged.
- * K is written as bf16, or as fp32 with k_fp32 = 1 (the dtype the reference
- * returns for a bf16 source and fp32 cos / sin).  Z, K, V, dZ use g4_layout
- * element strides (K's in its own dtype); rows are (batch, token, head).
- * cos / sin are fp32 (batch, seqlen, rotary_dim), rows contiguous, batch
- * stride cs_batch_stride elements (0: shared by every batch); the weight is
- * fp32 of head_dim.  head_dim must be 512; rotary_dim a multiple of 16 up to
- * 512.
+ *        rotary dims), other dims unchanged.
+ * K is written as fp32 with k_fp32 = 1 (the dtype the reference returns for a
+ * bf16 source and fp32 cos / sin: fp32 products and sum), or as bf16 with
+ * k_fp32 = 0 (bf16 source and tables: each product and the sum rounded to
+ * bf16, as bf16 tensor operations do).  Z, K, V, dZ use g4_layout element
+ * strides (K's in its own dtype); rows are (batch, token, head).  cos / sin
+ * are fp32 (batch, seqlen, rotary_dim), rows contiguous, batch stride
+ * cs_batch_stride elements (0: shared by every batch); the weight is fp32 of
+ * head_dim.  head_dim 512 or 256 (forward; the backward covers 512);
+ * rotary_dim a multiple of 16 up to head_dim.
  */
 typedef struct g4_kv_prep {
   int32_t num_batches;
@@ -250,7 +253,9 @@ typedef struct g4_kv_prep {
   int64_t cs_batch_stride;
 } g4_kv_prep;
 
-/* Forward: K, V from the source.  Stream-ordered, no workspace. */
+/* Forward: K, V from the source; either output may be NULL (not written:
+ * queries are prepared as K alone, a separate value projection as V alone).
+ * Stream-ordered, no workspace. */
 int g4_kv_prep_fwd(const g4_kv_prep* p,
                    const void* z, g4_layout z_layout,
                    const float* weight, const float* cos, const float* sin,

@@ -363,3 +363,32 @@ def test_backward_budget_drops_stored_ds_before_failing(monkeypatch):
     monkeypatch.setattr(att, "_free_hbm", lambda _d: free_for(lean - 1))
     with pytest.raises(g.GlobalBackwardBudgetExceeded):
         att._preflight_backward(plan, q, k, v)
+
+
+def test_row_preparation_validation_happens_before_any_launch():
+    # Host-side checks of g4_kv_prep_fwd / _bwd with fake addresses: nothing
+    # reaches the device when a check fails.
+    import ctypes
+    lib = _lib.load()
+    lay = _lib.G4Layout(0, 16 * 256, 256)
+    p = _lib.G4KvPrep(num_batches=1, seqlen=4, num_heads=16, head_dim=256, rotary_dim=256,
+                      k_fp32=0, eps=1e-6, cs_batch_stride=0)
+    assert lib.g4_kv_prep_fwd(ctypes.byref(p), 0x1000, lay, 0x2000, 0x3000, 0x4000, None, lay,
+                              None, lay, None) == _lib.G4_ERR_INVALID
+    assert b"both K and V are NULL" in lib.g4_last_error()
+    # a K output needs the rotary tables; a V-only call does not
+    assert lib.g4_kv_prep_fwd(ctypes.byref(p), 0x1000, lay, 0x2000, None, None, 0x5000, lay,
+                              None, lay, None) == _lib.G4_ERR_INVALID
+    assert b"cos and sin" in lib.g4_last_error()
+    assert lib.g4_kv_prep_fwd(ctypes.byref(p), 0x1000, lay, 0x2003, None, None, None, lay,
+                              0x6000, lay, None) == _lib.G4_ERR_INVALID
+    assert b"weight" in lib.g4_last_error()
+    odd = _lib.G4KvPrep(num_batches=1, seqlen=4, num_heads=16, head_dim=384, rotary_dim=0,
+                        k_fp32=0, eps=1e-6, cs_batch_stride=0)
+    assert lib.g4_kv_prep_fwd(ctypes.byref(odd), 0x1000, lay, 0x2000, None, None, None, lay,
+                              0x6000, lay, None) == _lib.G4_ERR_UNSUPPORTED
+    # the backward covers head_dim 512 only
+    assert lib.g4_kv_prep_bwd(ctypes.byref(p), 0x1000, lay, 0x2000, 0x3000, 0x4000, 0x5000, lay,
+                              0x6000, lay, 0x7000, lay, 0x8000, 0x9000, 1 << 20,
+                              None) == _lib.G4_ERR_UNSUPPORTED
+    assert b"head_dim 512" in lib.g4_last_error()
