@@ -480,6 +480,11 @@ __device__ __forceinline__ void acc_prologue(const TR& trd, const char G4_LDS* t
     acc_prologue<NB, A, N + 1>(trd, t, x);
   }
 }
+// While a wave issues an MFMA chain it runs at raised priority, so that when
+// the two waves of a SIMD are both ready the matrix core is fed first.
+__device__ __forceinline__ void mfma_prio_begin() { __builtin_amdgcn_s_setprio(1); }
+__device__ __forceinline__ void mfma_prio_end() { __builtin_amdgcn_s_setprio(0); }
+
 template <int NB, int A = kAhead, class TR>
 __device__ __forceinline__ void acc_steps(const TR& trd, const char G4_LDS* t,
                                           const bf16x8 (&b)[2], f32x16 (&acc)[NB]) {
@@ -487,7 +492,9 @@ __device__ __forceinline__ void acc_steps(const TR& trd, const char G4_LDS* t,
   bf16x8 x[A];
   acc_prologue<NB, A, 0>(trd, t, x);
   __builtin_amdgcn_sched_barrier(0);
+  mfma_prio_begin();
   acc_pipe<NB, A, 0>(trd, t, b, acc, x);
+  mfma_prio_end();
 }
 
 // part += (tile rows)[32 x 16 CP ...] . frag[CP], over CP in [0, NC).
@@ -516,7 +523,9 @@ __device__ __forceinline__ void row_steps(const RR& rrd, const char G4_LDS* t, f
   bf16x8 x[A];
   row_prologue<A, 0>(rrd, t, x);
   __builtin_amdgcn_sched_barrier(0);
+  mfma_prio_begin();
   row_pipe<NC, A, 0>(rrd, t, part, frag, x);
+  mfma_prio_end();
 }
 
 }  // namespace g4

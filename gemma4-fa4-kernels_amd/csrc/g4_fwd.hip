@@ -161,6 +161,8 @@ struct FwdKernel {
     f32x16 sacc[C::kKB];
     const char G4_LDS* kt = smem + C::kLdsK + cur * C::kTileBytes;
     __builtin_amdgcn_sched_barrier(0);
+    mfma_prio_begin();
+    __builtin_amdgcn_sched_barrier(0);
     sacc[0] = f32x16{};
     s_step<0, 0>(kt, sacc[0]);
     if constexpr (C::kKB > 1) {
@@ -169,6 +171,8 @@ struct FwdKernel {
     }
     mfma_pipeline_hint<C::kKB * kNC, 3, 1>();
 
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_prio_end();
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (DSPLIT > 1) {
       // Publish the partial, then add the partner slice's partial.
@@ -252,6 +256,8 @@ struct FwdKernel {
     // O^T += V^T P^T with V^T from transposing reads of the V tile.
     const char G4_LDS* vt = smem + C::kLdsV + (VDOUBLE ? cur : 0) * C::kTileBytes;
     __builtin_amdgcn_sched_barrier(0);
+    mfma_prio_begin();
+    __builtin_amdgcn_sched_barrier(0);
     pv_step<0, 0, 0>(vt, pb[0][0]);
     pv_step<0, 1, 0>(vt, pb[0][1]);
     if constexpr (C::kKB > 1) {
@@ -260,6 +266,8 @@ struct FwdKernel {
     }
     mfma_pipeline_hint<C::kKB * 2 * kNB, 6, 2>();
 
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_prio_end();
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (!VDOUBLE) {
       // Single V buffer: every wave must finish its PV reads before refill.
