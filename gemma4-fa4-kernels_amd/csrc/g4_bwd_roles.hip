@@ -1689,7 +1689,7 @@ __global__ void __launch_bounds__(DqDsCfg<D>::kNT, 1) dq_ds_kernel(BwdParams a) 
 template <int D>
 static hipError_t launch_dq_ds(const BwdParams& a, hipStream_t stream) {
   using C = DqDsCfg<D>;
-  static bool done[2] = {false, false};
+  static LdsAttr attr[2];
   BwdParams b = a;
   b.ntiles = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
   const int64_t items = (int64_t)b.num_seqs * b.ntiles * a.p.num_q_heads;
@@ -1700,12 +1700,8 @@ static hipError_t launch_dq_ds(const BwdParams& a, hipStream_t stream) {
       grid.size((const void*)dq_ds_kernel<D, true>, C::kNT, C::kLdsBytes, items, &queue);
   if (nblocks <= 0) return hipErrorInvalidValue;
   void (*kern)(BwdParams) = queue ? dq_ds_kernel<D, true> : dq_ds_kernel<D, false>;
-  if (!done[queue]) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
-    if (e != hipSuccess) return e;
-    done[queue] = true;
-  }
+  hipError_t e = attr[queue].ensure((const void*)kern, C::kLdsBytes);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();
 }
@@ -1733,14 +1729,9 @@ hipError_t launch_dq_roles_d(const BwdParams& a, hipStream_t stream) {
     kern = meta ? (queue ? dq_roles256_kernel<true, true> : dq_roles256_kernel<true, false>)
                 : (queue ? dq_roles256_kernel<false, true> : dq_roles256_kernel<false, false>);
   }
-  static bool done[4] = {false, false, false, false};
-  const int v = 2 * meta + queue;
-  if (!done[v]) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
-    if (e != hipSuccess) return e;
-    done[v] = true;
-  }
+  static LdsAttr attr[4];
+  hipError_t e = attr[2 * meta + queue].ensure((const void*)kern, C::kLdsBytes);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();
 }
@@ -1792,14 +1783,9 @@ hipError_t launch_dkdv_roles_d(const BwdParams& a, hipStream_t stream) {
   const int64_t nblocks = grid.size((const void*)kq[meta], C::kNT, C::kLdsBytes, items, &queue);
   if (nblocks <= 0) return hipErrorInvalidValue;
   void (*kern)(BwdParams) = queue ? kq[meta] : ks[meta];
-  static bool done[4] = {false, false, false, false};
-  const int v = 2 * meta + queue;
-  if (!done[v]) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
-    if (e != hipSuccess) return e;
-    done[v] = true;
-  }
+  static LdsAttr attr[4];
+  hipError_t e = attr[2 * meta + queue].ensure((const void*)kern, C::kLdsBytes);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();
 }

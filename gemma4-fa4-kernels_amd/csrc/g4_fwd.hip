@@ -690,13 +690,9 @@ __global__ void __launch_bounds__(256, 1) fwd_wide_kernel(FwdParams a) {
 template <int D>
 static hipError_t launch_fwd_wide(const FwdParams& a, hipStream_t stream) {
   using C = WideCfg<D>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)fwd_wide_kernel<D>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static LdsAttr attr;
+  hipError_t e = attr.ensure((const void*)fwd_wide_kernel<D>, C::kLdsBytes);
+  if (e != hipSuccess) return e;
   FwdParams b = a;
   b.ntq = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
   const int64_t nblocks = (int64_t)b.num_seqs * b.ntq * a.p.num_q_heads;
@@ -725,13 +721,9 @@ static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fi
       : fixup     ? fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, 0, true, OCC>
                   : fwd_kernel<D, BN, DSPLIT, NQG, VDOUBLE, 0, false, OCC>;
   const int variant = fixup ? 4 : meta;
-  static bool attr_set[5] = {false, false, false, false, false};
-  if (!attr_set[variant]) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::kLdsBytes);
-    if (e != hipSuccess) return e;
-    attr_set[variant] = true;
-  }
+  static LdsAttr attr[5];
+  hipError_t e = attr[variant].ensure((const void*)kern, C::kLdsBytes);
+  if (e != hipSuccess) return e;
   FwdParams b = a;
   b.ntq = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
   b.doc_pass = doc_pass;

@@ -76,6 +76,30 @@ size_t delta_bytes(const g4_problem& p);
 size_t raise_flags_bytes(const g4_problem& p);
 constexpr size_t kSchedBytes = 256;  // work-queue counters (backward workspace tail)
 
+// Function attributes and occupancy are per device, and one process may drive
+// several GPUs: launch-time state is cached per device (the current device,
+// which the caller keeps equal to the stream's device, as for any HIP launch).
+constexpr int kMaxDevices = 64;
+
+__host__ inline int current_device() {
+  int dev = 0;
+  return hipGetDevice(&dev) == hipSuccess ? dev : -1;
+}
+
+// Dynamic-LDS limit of one kernel, raised once per device.
+struct LdsAttr {
+  std::atomic<int> set[kMaxDevices] = {};
+  hipError_t ensure(const void* kern, int bytes) {
+    const int dev = current_device();
+    const bool cached = dev >= 0 && dev < kMaxDevices;
+    if (cached && set[dev].load(std::memory_order_acquire)) return hipSuccess;
+    const hipError_t e =
+        hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess && cached) set[dev].store(1, std::memory_order_release);
+    return e;
+  }
+};
+
 // Launch shape of a tile kernel with a work-queue variant: with more than
 // kQueueMin items per resident workgroup (CUs x workgroups per CU from the
 // occupancy query of the queue variant) the queue variant on as many
@@ -85,19 +109,21 @@ constexpr size_t kSchedBytes = 256;  // work-queue counters (backward workspace 
 // configs 1 and 3).
 struct PersistentGrid {
   static constexpr int kQueueMin = 4;
-  std::atomic<int> resident{0};
+  std::atomic<int> resident[kMaxDevices] = {};  // per device; 0 until queried
   // Workgroups of the launch; *queue says which variant.
   int64_t size(const void* queue_kern, int threads, int lds, int64_t items, bool* queue) {
-    int n = resident.load(std::memory_order_relaxed);
+    const int dev = current_device();
+    if (dev < 0) return 0;
+    const bool cached = dev < kMaxDevices;
+    int n = cached ? resident[dev].load(std::memory_order_relaxed) : 0;
     if (n == 0) {
-      int dev = 0, cus = 0, per_cu = 0;
-      if (hipGetDevice(&dev) != hipSuccess ||
-          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      int cus = 0, per_cu = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
           hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, queue_kern, threads, lds) !=
               hipSuccess)
         return 0;
       n = cus * (per_cu > 1 ? per_cu : 1);
-      resident.store(n, std::memory_order_relaxed);
+      if (cached) resident[dev].store(n, std::memory_order_relaxed);
     }
     *queue = items > (int64_t)kQueueMin * n;
     return *queue ? n : items;
