@@ -100,7 +100,7 @@ def run_workload(torch, g, w, *, steps: int, warmup: int, dev, flush=None):
     """
     from gemma4_fa4_amd import workloads as wl
 
-    q, k, v, do, cu, vis, docs = wl.tensors(w, dev)
+    q, k, v, do, cu, vis, docs = wl.tensors(w, dev, device_rng=w.device_rng)
     mq = max(w.seg_lengths)
     if w.kind == "local":
         def attn(qi, ki, vi):
@@ -408,7 +408,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true",
                     help="only configuration 2 (skip configurations 1, 3, 4, 5 and the cold-cache run)")
     ap.add_argument("--extra-configs", default="1,3,4,5",
-                    help="comma-separated configurations timed besides configuration 2")
+                    help="comma-separated configurations timed besides configuration 2 "
+                         "(6: a 65536-token global sequence, on request only)")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache run")
     args = ap.parse_args()
     if args.gpus != 1:

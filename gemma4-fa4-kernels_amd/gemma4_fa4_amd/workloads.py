@@ -43,6 +43,7 @@ class Workload:
     documents: np.ndarray | None = None  # int32 per token
     seed: int = 0
     notes: dict = field(default_factory=dict)
+    device_rng: bool = False  # draw the operands on the device (very large workloads)
 
     @property
     def hq(self) -> int:
@@ -136,6 +137,15 @@ def config5(seed: int = 5) -> Workload:
     return Workload("config5_packed_local_d256_T131072_vision_docs_fwd_bwd", "local",
                     [int(x) for x in lengths], ("fwd", "bwd", "fwd_bwd"), vision=vision,
                     documents=documents, seed=seed)
+
+
+def config6(seed: int = 6) -> Workload:
+    """Long context (not a BASELINE configuration): one global d512 causal sequence of
+    65536 tokens, the reference's S64K row (EXP-0035:69-70).  Its dense stored-dS
+    buffer (256 GiB) exceeds the default budget, so the backward recomputes S and dP
+    in the dQ stage."""
+    return Workload("config6_global_d512_S65536_fwd_bwd", "global", [65536],
+                    ("fwd", "bwd", "fwd_bwd"), seed=seed, device_rng=True)
 
 
 ALL_CONFIGS = (config1, config2, config3, config4, config5)
