@@ -8,6 +8,7 @@ is an error, never a fallback.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -129,6 +130,9 @@ _lib: ctypes.CDLL | None = None
 def load(path: str | None = None) -> ctypes.CDLL:
     """Load (once) and return the HIP library; raise if it is not built."""
     global _lib
+    lib = _lib
+    if lib is not None:
+        return lib
     with _lock:
         if _lib is not None:
             return _lib
@@ -148,6 +152,19 @@ def load(path: str | None = None) -> ctypes.CDLL:
             raise UnsupportedMI355XPath(f"library ABI {version} != expected {ABI_VERSION}")
         _lib = lib
         return lib
+
+
+def device_scope(device: torch.device):
+    """A guard that makes ``device`` current for a launch (none when it already is)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
+
+
+def raw_stream(device: torch.device) -> int:
+    """The handle of torch's current stream on ``device`` (its ``cuda_stream``)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def check(rc: int) -> None:

@@ -44,18 +44,36 @@ _TARGET_ARCH = "gfx950"
 # ---------------------------------------------------------------------------
 
 
+_FAKE_TENSOR_TYPE: list = []
+
+
+def _fake_tensor_type():
+    if not _FAKE_TENSOR_TYPE:
+        try:
+            from torch._subclasses.fake_tensor import FakeTensor
+        except ImportError:  # pragma: no cover
+            FakeTensor = ()
+        _FAKE_TENSOR_TYPE.append(FakeTensor)
+    return _FAKE_TENSOR_TYPE[0]
+
+
 def _is_fake_tensor(tensor: torch.Tensor) -> bool:
-    try:
-        from torch._subclasses.fake_tensor import FakeTensor
-    except ImportError:  # pragma: no cover
-        return False
-    return isinstance(tensor, FakeTensor)
+    return isinstance(tensor, _fake_tensor_type())
+
+
+# gcnArchName per device index: a device's architecture does not change while
+# the process runs, and the property query costs a few microseconds per call.
+_DEVICE_ARCH: dict[int, str] = {}
 
 
 def _require_gfx950(device: torch.device) -> None:
     if device.type != "cuda":
         raise UnsupportedMI355XPath("MI355X attention inputs must be GPU tensors")
-    arch = torch.cuda.get_device_properties(device).gcnArchName
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    arch = _DEVICE_ARCH.get(index)
+    if arch is None:
+        arch = torch.cuda.get_device_properties(index).gcnArchName
+        _DEVICE_ARCH[index] = arch
     if not arch.startswith(_TARGET_ARCH):
         raise UnsupportedMI355XPath(f"MI355X attention requires {_TARGET_ARCH}, found {arch}")
 
@@ -78,22 +96,27 @@ def _has_proven_nonoverlap(tensor: torch.Tensor) -> bool:
 
 
 def _validate_layout(tensor: torch.Tensor, *, name: str) -> None:
-    if tensor.stride(-1) != 1:
+    strides = tensor.stride()
+    if strides[-1] != 1:
         raise ValueError(f"{name} must have unit last-dimension stride")
-    if any(stride <= 0 for stride in tensor.stride()):
+    if min(strides) <= 0:
         raise ValueError(f"{name} must use positive, non-broadcast strides")
-    if any(stride % 8 for stride in tensor.stride()[:-1]):
-        raise ValueError(f"{name} outer strides must be 16-byte aligned for BF16")
+    for stride in strides[:-1]:
+        if stride % 8:
+            raise ValueError(f"{name} outer strides must be 16-byte aligned for BF16")
     if not _has_proven_nonoverlap(tensor):
         raise ValueError(f"{name} must use a non-overlapping layout")
 
 
 def _check_real_operands(tensors, names, *, label: str) -> None:
-    fake = [_is_fake_tensor(t) for t in tensors]
-    if any(fake):
-        raise UnsupportedMI355XPath(f"{label}: fake tensors are not supported by the MI355X path")
-    if any(t.data_ptr() % 16 for t in tensors):
-        raise ValueError(f"{label} base pointers must be 16-byte aligned")
+    fake_type = _fake_tensor_type()
+    for t in tensors:
+        if isinstance(t, fake_type):
+            raise UnsupportedMI355XPath(
+                f"{label}: fake tensors are not supported by the MI355X path")
+    for t in tensors:
+        if t.data_ptr() % 16:
+            raise ValueError(f"{label} base pointers must be 16-byte aligned")
 
 
 def _validate_bshd(q, k, v, spec: AttentionLayerSpec, *, require_device: bool = True) -> None:
@@ -295,37 +318,45 @@ def _cumulative_lengths(cu_q, cu_k, q, k, *, label: str):
         raise ValueError(f"{label} cumulative arrays must end at the packed Q/K totals")
     q_lengths = [e - s for s, e in zip(q_vals[:-1], q_vals[1:])]
     k_lengths = [e - s for s, e in zip(k_vals[:-1], k_vals[1:])]
-    if any(length < 0 for length in (*q_lengths, *k_lengths)):
+    if min(q_lengths) < 0 or min(k_lengths) < 0:
         raise ValueError(f"{label} cumulative arrays must be nondecreasing")
     return q_lengths, k_lengths
 
 
+def _is_python_int(x) -> bool:
+    return type(x) is int or (isinstance(x, int) and not isinstance(x, bool))
+
+
 def _validate_packed_common(q, k, v, cu_q, cu_k, max_q, max_k, *, label: str):
-    if any(t.ndim != 3 for t in (q, k, v)):
+    # Written as plain comparisons (no generator expressions): these checks run
+    # on every call, ahead of the launch.
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
         raise ValueError(f"{label} q, k, and v must be rank-3 T/H/D tensors")
-    if not (q.device == k.device == v.device):
+    device = q.device
+    if not (device == k.device == v.device):
         raise ValueError(f"{label} q, k, and v must be on one device")
-    if any(t.dtype != torch.bfloat16 for t in (q, k, v)):
+    bf16 = torch.bfloat16
+    if q.dtype != bf16 or k.dtype != bf16 or v.dtype != bf16:
         raise ValueError(f"{label} q, k, and v must use BF16")
     if q.shape[0] <= 0 or k.shape[0] <= 0:
         raise ValueError(f"{label} Q and K totals must be positive")
-    for name, tensor in zip(("packed q", "packed k", "packed v"), (q, k, v)):
-        _validate_layout(tensor, name=name)
+    _validate_layout(q, name="packed q")
+    _validate_layout(k, name="packed k")
+    _validate_layout(v, name="packed v")
     _check_real_operands((q, k, v), ("q", "k", "v"), label=f"{label} q, k, and v")
     if k.untyped_storage().data_ptr() == v.untyped_storage().data_ptr():
         raise ValueError("K and V must be distinct, non-aliasing prepared operands")
-    if any(isinstance(x, bool) or not isinstance(x, int) for x in (max_q, max_k)):
+    if not (_is_python_int(max_q) and _is_python_int(max_k)):
         raise TypeError("max_seqlen_q and max_seqlen_k must be Python integers")
-    cumulative = (cu_q, cu_k)
-    if any(t.ndim != 1 or t.numel() < 2 for t in cumulative):
+    if cu_q.ndim != 1 or cu_q.numel() < 2 or cu_k.ndim != 1 or cu_k.numel() < 2:
         raise ValueError("cu_seqlens_q and cu_seqlens_k must be rank-1 B+1 tensors")
     if cu_q.shape != cu_k.shape:
         raise ValueError("cu_seqlens_q and cu_seqlens_k must have the same batch count")
-    if any(t.device != q.device for t in cumulative):
+    if cu_q.device != device or cu_k.device != device:
         raise ValueError("cu_seqlens_q and cu_seqlens_k must share the q/k/v device")
-    if any(t.dtype != torch.int32 for t in cumulative):
+    if cu_q.dtype != torch.int32 or cu_k.dtype != torch.int32:
         raise ValueError("cu_seqlens_q and cu_seqlens_k must use INT32")
-    if any(not t.is_contiguous() for t in cumulative):
+    if not (cu_q.is_contiguous() and cu_k.is_contiguous()):
         raise ValueError("cu_seqlens_q and cu_seqlens_k must be contiguous")
 
 
@@ -537,29 +568,31 @@ class _Plan:
             return (self.num_q_heads, self.total_q)
         return (self.num_seqs, self.num_q_heads, self.seqlen_q)
 
-    def workspace_bytes(self, phase: int) -> int:
+    def workspace_bytes(self, phase: int, prob: G4Problem | None = None) -> int:
         lib = _lib.load()
-        prob = self.problem()
+        if prob is None:
+            prob = self.problem()
         nbytes = lib.g4_workspace_bytes(ctypes.byref(prob), phase)
         if nbytes == 0 and lib.g4_last_error():
             _lib.check(_lib.G4_ERR_INVALID)
         return int(nbytes)
 
-    def _workspace(self, phase: int, device) -> torch.Tensor:
-        return torch.empty(max(self.workspace_bytes(phase), 256), dtype=torch.uint8, device=device)
+    def _workspace(self, phase: int, device, prob: G4Problem | None = None) -> torch.Tensor:
+        nbytes = max(self.workspace_bytes(phase, prob), 256)
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
     def forward(self, q, k, v):
         try:
             lib = _lib.load()
+            prob = self.problem()
             out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
             lse = torch.empty(self.lse_shape(), dtype=torch.float32, device=q.device)
-            ws = self._workspace(0, q.device)
+            ws = self._workspace(0, q.device, prob)
         except Exception:
             self._settle()  # an invalid cu_seqlens is reported first
             raise
-        prob = self.problem()
-        with torch.cuda.device(q.device):
-            stream = torch.cuda.current_stream(q.device).cuda_stream
+        with _lib.device_scope(q.device):
+            stream = _lib.raw_stream(q.device)
             args = (
                 ctypes.byref(prob),
                 q.data_ptr(), _layout(q, self.packed),
@@ -583,10 +616,10 @@ class _Plan:
         dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
         dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
-        ws = self._workspace(1, q.device)
         prob = self.problem()
-        with torch.cuda.device(q.device):
-            stream = torch.cuda.current_stream(q.device).cuda_stream
+        ws = self._workspace(1, q.device, prob)
+        with _lib.device_scope(q.device):
+            stream = _lib.raw_stream(q.device)
             rc = lib.g4_attn_bwd(
                 ctypes.byref(prob),
                 q.data_ptr(), _layout(q, self.packed),
