@@ -90,7 +90,7 @@ def _stats(samples):
     return {"median": statistics.median(samples), "p25": q[0], "p75": q[2]}
 
 
-def run_workload(torch, g, w, *, steps: int, warmup: int, dev, flush=None):
+def run_workload(torch, g, w, *, steps: int, warmup: int, dev, flush=None, kernel_only=True):
     """Time the timed modes of one workload through the drop-in packed adapters.
 
     fwd: forward with autograd off; bwd: torch.autograd.backward of a forward
@@ -158,6 +158,24 @@ def run_workload(torch, g, w, *, steps: int, warmup: int, dev, flush=None):
         res[f"{mode}_ms_p25_p75"] = [round(st["p25"], 4), round(st["p75"], 4)]
         res[f"{mode}_tflops"] = round(tf, 2)
         res[f"{mode}_pct_peak"] = round(100.0 * tf / PEAK_BF16_TFLOPS, 2)
+    if not kernel_only:
+        return res, (q, k, v, do, cu)
+    # The forward launched through the C ABI alone (no adapter validation,
+    # planning or output allocation): the kernels' time, beside the per-call
+    # figures above, which include the adapter's host work.
+    from gemma4_fa4_amd import ops
+    from gemma4_fa4_amd.attention import _packed_plan
+
+    spec = g.GLOBAL_ATTENTION if w.kind == "global" else g.SLIDING_ATTENTION
+    plan = _packed_plan(q, k, cu, cu, mq, mq, spec, vision=vis, documents=docs)
+    st = ops.Stages(plan, q, k, v, do, forward_only=True)
+    kst = _stats(event_times(torch, st.forward, max(steps, 3), max(warmup, 1)))
+    tf = flops(pairs, w.hq, w.d, "fwd") / (kst["median"] * 1e-3) / 1e12
+    res["fwd_kernel_ms"] = round(kst["median"], 4)
+    res["fwd_kernel_ms_p25_p75"] = [round(kst["p25"], 4), round(kst["p75"], 4)]
+    res["fwd_kernel_tflops"] = round(tf, 2)
+    res["fwd_kernel_pct_peak"] = round(100.0 * tf / PEAK_BF16_TFLOPS, 2)
+    del st
     return res, (q, k, v, do, cu)
 
 
@@ -436,7 +454,8 @@ def main() -> int:
             # Cold caches: a 1 GiB write (4x the 256 MB Infinity Cache) before each call.
             junk = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
             cold, _ = run_workload(torch, g, wl.config2(), steps=max(3, args.steps // 2),
-                                   warmup=1, dev=dev, flush=lambda: junk.fill_(1))
+                                   warmup=1, dev=dev, flush=lambda: junk.fill_(1),
+                                   kernel_only=False)
             head["fwd_bwd_cold_ms"] = cold["fwd_bwd_ms"]
             head["fwd_bwd_cold_tflops"] = cold["fwd_bwd_tflops"]
             del junk

@@ -227,18 +227,31 @@ struct TileCopier {
   __device__ __forceinline__ void issue(const __bf16* tile_row0, char G4_LDS* tile) const {
     const char* g = (const char*)tile_row0;
     const int ln = fresh_lane();
-    const int lr = ln / CPR, lc = ln % CPR;
-    const uint32_t lane_row = (uint32_t)lr * (uint32_t)stride_bytes;
+    if constexpr (CPR == 64) {
+      // one row per instruction: the slot is lane ^ swz(row)
+      const int lr = ln / CPR, lc = ln % CPR;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int u = i * NW + wave;
-      const int r = u * kRows + lr;
-      const uint32_t c = lc ^ (((r & 3) << 2) | ((r >> 2) & 3));
-      const char* row = g + (int64_t)(u * kRows) * stride_bytes;
-      if constexpr (CPR == 64)
-        g2l16(row + c * 16u, tile + u * 1024);  // lane_row == 0: offset is lane ^ const
-      else
-        b2l16(row, lane_row + c * 16u, tile + u * 1024);
+      for (int i = 0; i < kPer; ++i) {
+        const int u = i * NW + wave;
+        const int r = u * kRows + lr;
+        const uint32_t c = lc ^ (((r & 3) << 2) | ((r >> 2) & 3));
+        const char* row = g + (int64_t)(u * kRows) * stride_bytes;
+        g2l16(row + c * 16u, tile + u * 1024);
+      }
+    } else {
+      // Two rows per instruction: lane row lr = ln >> 5, row r = 2u + lr.  As 2u
+      // is even, swz(r) = swz(2u) ^ (lr << 2), so the slot (ln & 31) ^ swz(r)
+      // is a lane constant XOR a wave-uniform value: one v_xad_u32 per copy.
+      const int lr = ln >> 5;
+      const uint32_t lane16 = (uint32_t)(((ln & 31) ^ (lr << 2)) << 4);
+      const uint32_t lane_row = lr ? (uint32_t)stride_bytes : 0u;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int u = i * NW + wave;
+        const int r = 2 * u;
+        const uint32_t s16 = (uint32_t)((((r & 3) << 2) | ((r >> 2) & 3)) << 4);
+        b2l16(g + (int64_t)r * stride_bytes, (lane16 ^ s16) + lane_row, tile + u * 1024);
+      }
     }
   }
   // Tail tile: rows >= nrows are replaced by row nrows - 1 (their scores are

@@ -209,13 +209,11 @@ struct FwdKernel {
     }
 
     // Mask (only on tiles the mask does not fully admit), then online softmax
-    // in the log2 domain (softmax scale is 1.0).
+    // in the log2 domain (softmax scale is 1.0; log2 e is folded into the
+    // exponent's FMA, and the row maximum is scaled once: rounding is
+    // monotonic, so max(s) * log2 e rounds to the maximum of the scaled scores).
     const bool full = !has_doc && (kb0 + BN <= sq.lk) && (kb0 + BN - 1 <= a0) &&
                       (p->window <= 0 || kb0 > a0 + C::kBM - 1 - p->window);
-#pragma unroll
-    for (int kb = 0; kb < C::kKB; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kb][r] *= kLog2e;
     if (!full) {
       __builtin_amdgcn_sched_barrier(0);
       apply_mask(cur, sacc, kb0);
@@ -226,7 +224,7 @@ struct FwdKernel {
     for (int kb = 0; kb < C::kKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-    mx = fmaxf(mx, wave_xor32(mx));
+    mx = fmaxf(mx, wave_xor32(mx)) * kLog2e;
     // The running maximum only moves when a row's scores exceed it by more
     // than kRescaleLog2 (P <= 2^kRescaleLog2 meanwhile, exact in fp32 and in
     // bf16 range), so the O accumulators are rescaled rarely after the first
@@ -242,7 +240,7 @@ struct FwdKernel {
       for (int hk = 0; hk < 2; ++hk)
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-          float pv = fast_exp2(sacc[kb][hk * 8 + m] - m_use);
+          float pv = fast_exp2(__builtin_fmaf(sacc[kb][hk * 8 + m], kLog2e, -m_use));
           rs += pv;
           pb[kb][hk][m] = (__bf16)pv;
         }
@@ -405,9 +403,10 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a
   ker.m_run = kNegInf;
   ker.l_run = 0.f;
 
-  for (int it = 0; it < ntiles; ++it) {
-    ker.step(it & 1, it, ntiles, t_first);
-  }
+  // Two tiles per iteration, so each step's buffers are compile-time.
+  // (Two tiles per iteration with compile-time buffers measured slower: the
+  // unrolled loop spills.)
+  for (int it = 0; it < ntiles; ++it) ker.step(it & 1, it, ntiles, t_first);
 
   // ---- epilogue: normalise, write O and LSE ---------------------------------
   const float l_tot = ker.l_run + wave_xor32(ker.l_run);

@@ -92,7 +92,8 @@ class Stages:
     stream-ordered library call on the current stream.
     """
 
-    def __init__(self, plan: _Plan, q, k, v, dout, dlse=None):
+    def __init__(self, plan: _Plan, q, k, v, dout, dlse=None, *, forward_only: bool = False):
+        """``forward_only``: size the workspace for the forward launch alone."""
         from .attention import _layout
 
         self.plan = plan
@@ -103,7 +104,8 @@ class Stages:
         self.dq = torch.empty_like(q)
         self.dk = torch.empty_like(k)
         self.dv = torch.empty_like(v)
-        self.ws = torch.empty(max(plan.workspace_bytes(1), 256), dtype=torch.uint8, device=dev)
+        phase = 0 if forward_only else 1
+        self.ws = torch.empty(max(plan.workspace_bytes(phase), 256), dtype=torch.uint8, device=dev)
         self.prob = plan.problem()
         self.lay = {name: _layout(t, plan.packed) for name, t in (
             ("q", q), ("k", k), ("v", v), ("o", self.o), ("do", dout), ("dq", self.dq),
