@@ -111,7 +111,8 @@ struct RolesCfg {
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 };
 
-template <bool META>
+// ROT: the dh = 1 P waves read the Q tile rotated by 16 rows (see step_p).
+template <bool META, bool ROT>
 struct RolesKernel {
   using C = RolesCfg;
   char G4_LDS* smem;
@@ -197,8 +198,12 @@ struct RolesKernel {
     if (it + 1 < nsteps) issue_q(it + 1, cur ^ 1);
     row_steps(rrd, qt, sp, frag);
     __builtin_amdgcn_sched_barrier(0);
-    // the partner's rows of this partial
-    const int po = 8 * (dh ^ 1);
+    // the partner's rows of this partial.  With ROT, registers 8-15 in both
+    // waves (the dh = 1 wave reads the Q tile rotated by 16 rows, so its own
+    // rows, like the dh = 0 wave's, are in registers 0-7); without, the
+    // register index depends on dh, a runtime index (s_set_gpr_idx moves).
+    const int po = ROT ? 8 : 8 * (dh ^ 1);
+    const int mo = ROT ? 0 : 8 * dh;
 #pragma unroll
     for (int q4 = 0; q4 < 2; ++q4)
       *(f32x4 G4_LDS*)xs(slot ^ 1, q4) =
@@ -209,7 +214,6 @@ struct RolesKernel {
     const bool full = !has_doc && (i0 + C::kBM <= sq.lq) && (j0 + C::kBN <= sq.lk) &&
                       (j0 + C::kBN - 1 <= i0 + off) &&
                       (a->p.window <= 0 || j0 > i0 + C::kBM - 1 + off - a->p.window);
-    const int mo = 8 * dh;
 #pragma unroll
     for (int q4 = 0; q4 < 2; ++q4) {
       const f32x4 theirs = *(const f32x4 G4_LDS*)xs(slot, q4);
@@ -365,7 +369,10 @@ struct RolesKernel {
 template <bool META, bool QUEUE>
 __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_raw, int kvh,
                                                 int s, int kt) {
-  using K = RolesKernel<META>;
+  // Rotation only in the one-item-per-workgroup launch: measured on config 2
+  // (one 8192-token sequence) dK/dV 5.32 -> 5.17 ms, but 5.21 -> 5.89 ms in the
+  // work-queue launch of config 4 (packed, 1-2048-token segments).
+  using K = RolesKernel<META, !QUEUE>;
   using C = RolesCfg;
   K ker;
   ker.smem = (char G4_LDS*)smem_raw;
@@ -431,6 +438,10 @@ __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_r
   ker.my_doc = ker.has_doc ? p.document_ids[sq.ktok + jc] : 0;
 
   ker.rrd.init(ker.lane, ker.dh * C::kDH * 2);
+  // P waves with dh = 1: Q rows rotated by 16 (row r ^ 16; the swizzle depends
+  // on r mod 16 only), so both waves of a pair hold their own rows of the S
+  // partial in accumulator registers 0-7.
+  if (!QUEUE && pwave && ker.dh) ker.rrd.base ^= 16 * C::kCPR * 16;
   ker.trd.init(ker.lane, ker.dh * C::kDH * 2);
   ker.qcp.init(a.ql.token_stride, ker.wave & 3, ker.lane);
   ker.docp.init(a.dol.token_stride, ker.wave & 3, ker.lane);
