@@ -1658,21 +1658,44 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
     }
   }
 
+  // dQ leaves through LDS: a lane's accumulators hold one query and 8-byte
+  // runs of the head dim, so storing them directly writes 8 bytes into each
+  // of 32 rows per instruction.  They are staged as bf16 rows of the
+  // 128-query tile (chunk c of row r at slot c ^ (r mod kCPR), which keeps the
+  // 32-row staging writes and the row reads free of bank conflicts) and
+  // written back as whole rows.  Band tiles keep queries in accumulator
+  // order, dense tiles in query order.
+  barrier_lds();  // every wave is done with the last key tile's operands
+  char G4_LDS* stage = ker.smem;
+  static_assert(C::kBM * C::kCPR * 16 <= C::kLdsBytes, "dQ staging tile");
 #pragma unroll
   for (int g2 = 0; g2 < 2; ++g2) {
-    // Band tiles keep queries in accumulator order, dense tiles in query order.
-    const int my_i = i0 + 32 * (g0 + g2) + (kBand ? ds_query_at(l32) : l32);
-    if (my_i >= sq.lq) continue;
-    __bf16* row = a.dq + tok_off(sq, s, sq.qtok, my_i, a.dql) + (int64_t)qh * a.dql.head_stride;
+    const int r = 32 * (g0 + g2) + (kBand ? ds_query_at(l32) : l32);
 #pragma unroll
     for (int b = 0; b < C::kNBw; ++b)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int d = ker.dquart * C::kDW + b * 32 + 8 * r4 + 4 * ker.h32;
         const f32x16& x = ker.acc[g2][b];
-        *(bf16x4*)(row + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
-                                     (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
+        *(bf16x4 G4_LDS*)(stage + (r * C::kCPR + ((d >> 3) ^ (r & (C::kCPR - 1)))) * 16 +
+                          (d & 4) * 2) =
+            bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1], (__bf16)x[r4 * 4 + 2],
+                   (__bf16)x[r4 * 4 + 3]};
       }
+  }
+  barrier_lds();
+  constexpr int kRowsPerInst = 64 / C::kCPR;
+#pragma unroll
+  for (int j = 0; j < C::kBM / (C::kNW * kRowsPerInst); ++j) {
+    const int r = (j * C::kNW + ker.wave) * kRowsPerInst + ker.lane / C::kCPR;
+    const int c = ker.lane % C::kCPR;
+    const int my_i = i0 + r;
+    if (my_i < sq.lq) {
+      const bf16x8 v =
+          *(const bf16x8 G4_LDS*)(stage + (r * C::kCPR + (c ^ (r & (C::kCPR - 1)))) * 16);
+      __bf16* row = a.dq + tok_off(sq, s, sq.qtok, my_i, a.dql) + (int64_t)qh * a.dql.head_stride;
+      *(bf16x8*)(row + c * 8) = v;
+    }
   }
 }
 
@@ -1682,12 +1705,25 @@ template <int D, bool QUEUE>
 __global__ void __launch_bounds__(DqDsCfg<D>::kNT, 1) dq_ds_kernel(BwdParams a) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   if constexpr (QUEUE) {
-    const int n = a.num_seqs * a.ntiles * a.p.num_q_heads;
-    WorkQueue wq{a.sched + 2, n, 0};
-    for (;;) {
-      const int t = wq.next((int G4_LDS*)smem_raw);
-      if (t >= n) break;
+    // The work queue's protocol (see WorkQueue), with each ticket drawn when
+    // the previous item starts, so the atomic's latency overlaps that item,
+    // and no wait for the item's dQ stores (they do not touch LDS; the item
+    // leaves no tile copy in flight).
+    const unsigned n = (unsigned)(a.num_seqs * a.ntiles * a.p.num_q_heads);
+    unsigned* counter = a.sched + 2;
+    int t = xcd_remap(blockIdx.x, gridDim.x);
+    while ((unsigned)t < n) {
+      unsigned old = 0;
+      if (threadIdx.x == 0) old = atomicAdd(counter, 1u);
       dq_ds_item<D, true>(a, smem_raw, t);
+      barrier_lds();  // every wave is done with the item's LDS
+      if (threadIdx.x == 0) {
+        if (old == n - 1u) atomicExch(counter, 0u);
+        *(int G4_LDS*)smem_raw = (int)(gridDim.x + old);
+      }
+      barrier_lds();
+      t = __builtin_amdgcn_readfirstlane(*(const int G4_LDS*)smem_raw);
+      barrier_lds();  // every wave has read the slot before the next item's copies
     }
   } else {
     dq_ds_item<D, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
