@@ -91,6 +91,7 @@ int check_ws(const g4_problem* p, int phase, void* ws, size_t bytes) {
   } while (0)
 
 // Workspace: [spans][raise flags] (forward); backward adds [delta][dS][queue counters]
+// [dQ recompute list]
 int* raise_flags_ptr(const g4_problem& p, void* ws) {
   return g4::raise_flags_bytes(p) ? (int*)((char*)ws + align256(g4::spans_bytes(p))) : nullptr;
 }
@@ -105,6 +106,10 @@ __bf16* ds_ptr(const g4_problem& p, void* ws) {
 unsigned* sched_ptr(const g4_problem& p, void* ws) {
   return (unsigned*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) +
                      g4::delta_bytes(p) + g4::ds_bytes(p));
+}
+int2* dq_list_ptr(const g4_problem& p, void* ws) {
+  if (!g4::dq_list_bytes(p)) return nullptr;
+  return (int2*)((char*)sched_ptr(p, ws) + g4::kSchedBytes);
 }
 
 // Forward workspace of g4_attn_fwd_static: a file-scope device array, one
@@ -230,6 +235,13 @@ size_t ds_bytes(const g4_problem& p) {
   const size_t b = (size_t)rows * cols * p.num_q_heads * 4096;
   return b <= ds_cap(p) ? b : 0;
 }
+// Head dim 256 stored-dS dQ with vision IDs: one 8-byte entry per possible
+// (sequence, 128-query tile, query head) for the tiles left to recompute.
+size_t dq_list_bytes(const g4_problem& p) {
+  if (p.head_dim != 256 || !ds_bytes(p) || p.vision_ids == nullptr || !p.bidirectional_vision)
+    return 0;
+  return align256((size_t)p.num_seqs * ((p.seqlen_q + 127) / 128) * p.num_q_heads * 8);
+}
 // One int per (sequence, 32-query group, query head) for the head-dim 512
 // forward's second pass.
 size_t raise_flags_bytes(const g4_problem& p) {
@@ -248,7 +260,8 @@ size_t g4_workspace_bytes(const g4_problem* p, int phase) {
   g_last_error.clear();
   if (check_problem(p) != G4_OK) return 0;
   size_t b = align256(g4::spans_bytes(*p)) + g4::raise_flags_bytes(*p);
-  if (phase == 1) b += g4::delta_bytes(*p) + g4::ds_bytes(*p) + g4::kSchedBytes;
+  if (phase == 1)
+    b += g4::delta_bytes(*p) + g4::ds_bytes(*p) + g4::kSchedBytes + g4::dq_list_bytes(*p);
   return b;
 }
 
@@ -291,6 +304,7 @@ static int fill_bwd(g4::BwdParams& a, const g4_problem* p, const void* q, g4_lay
   a.ds = ds_ptr(*p, ws);
   g4::ds_geometry(*p, &a.ds_rows, &a.ds_cols);
   a.sched = sched_ptr(*p, ws);
+  a.dq_list = dq_list_ptr(*p, ws);
   g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);
   return G4_OK;
 }

@@ -1263,19 +1263,30 @@ __device__ __forceinline__ void dq_roles256_item(const BwdParams& a, char* smem_
   const int l32 = ker.lane & 31;
 
   const int grp = p.num_q_heads / p.num_kv_heads;
-  const int per_kvh = a.num_seqs * a.ntiles * grp;
-  const int kvh = L / per_kvh;
-  const int rem = L % per_kvh;
-  const int rank = rem / grp;
-  const int qh = kvh * grp + rem % grp;
-  const int s = rank / a.ntiles;
-  const int qt = zigzag(rank % a.ntiles, a.ntiles);
+  int kvh, qh, s, qt;
+  const bool listed = a.dq_recompute_only && a.dq_list != nullptr;
+  if (listed) {
+    // Entry L of the stored-dS pass's list: a tile known to need recomputing.
+    const int2 e = a.dq_list[L];
+    s = __builtin_amdgcn_readfirstlane(e.x);
+    qt = __builtin_amdgcn_readfirstlane(e.y) >> 8;
+    qh = __builtin_amdgcn_readfirstlane(e.y) & 255;
+    kvh = qh / grp;
+  } else {
+    const int per_kvh = a.num_seqs * a.ntiles * grp;
+    kvh = L / per_kvh;
+    const int rem = L % per_kvh;
+    const int rank = rem / grp;
+    qh = kvh * grp + rem % grp;
+    s = rank / a.ntiles;
+    qt = zigzag(rank % a.ntiles, a.ntiles);
+  }
   ker.sq = resolve_seq(p, s);
   const Seq& sq = ker.sq;
   const int i0 = qt * C::kBM;
   if (i0 >= sq.lq) return;
   const int off = sq.lk - sq.lq;
-  if (a.dq_recompute_only) {
+  if (a.dq_recompute_only && !listed) {
     int kt_hi[4];
     if (!dq_row_key_ends<C::kNW>(a, sq, i0, off, tid, (int*)(smem_raw + C::kLdsRed), kt_hi))
       return;
@@ -1367,8 +1378,13 @@ __device__ __forceinline__ void dq_roles256_item(const BwdParams& a, char* smem_
 template <bool META, bool QUEUE>
 __global__ void __launch_bounds__(DqRoles256Cfg::kNT, 1) dq_roles256_kernel(BwdParams a) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  // The recompute launch after a stored-dS pass takes its items from that
+  // pass's list (at most one entry per query tile and head).
+  const int all = a.num_seqs * a.ntiles * a.p.num_q_heads;
+  const int n = a.dq_recompute_only && a.dq_list != nullptr
+                    ? min(__builtin_amdgcn_readfirstlane((int)a.sched[3]), all)
+                    : all;
   if constexpr (QUEUE) {
-    const int n = a.num_seqs * a.ntiles * a.p.num_q_heads;
     WorkQueue wq{a.sched + 2, n, 0};
     for (;;) {
       const int t = wq.next((int G4_LDS*)smem_raw);
@@ -1376,7 +1392,8 @@ __global__ void __launch_bounds__(DqRoles256Cfg::kNT, 1) dq_roles256_kernel(BwdP
       dq_roles256_item<META, true>(a, smem_raw, t);
     }
   } else {
-    dq_roles256_item<META, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
+    const int t = xcd_remap(blockIdx.x, gridDim.x);
+    if (t < n) dq_roles256_item<META, false>(a, smem_raw, t);
   }
 }
 
@@ -1595,7 +1612,14 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
   // start of its first query.
   int kt_hi[4];
   if constexpr (kBand) {
-    if (dq_row_key_ends<C::kNW>(a, sq, i0, off, tid, (int*)smem_raw, kt_hi)) return;
+    if (dq_row_key_ends<C::kNW>(a, sq, i0, off, tid, (int*)smem_raw, kt_hi)) {
+      // A row reaches past the stored band: left to the recompute launch.
+      if (tid == 0 && a.dq_list != nullptr) {
+        const unsigned e = atomicAdd(&a.sched[3], 1u);
+        a.dq_list[e] = int2{s, (qt << 8) | qh};
+      }
+      return;
+    }
   } else {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -1705,25 +1729,11 @@ template <int D, bool QUEUE>
 __global__ void __launch_bounds__(DqDsCfg<D>::kNT, 1) dq_ds_kernel(BwdParams a) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   if constexpr (QUEUE) {
-    // The work queue's protocol (see WorkQueue), with each ticket drawn when
-    // the previous item starts, so the atomic's latency overlaps that item,
-    // and no wait for the item's dQ stores (they do not touch LDS; the item
-    // leaves no tile copy in flight).
-    const unsigned n = (unsigned)(a.num_seqs * a.ntiles * a.p.num_q_heads);
-    unsigned* counter = a.sched + 2;
-    int t = xcd_remap(blockIdx.x, gridDim.x);
-    while ((unsigned)t < n) {
-      unsigned old = 0;
-      if (threadIdx.x == 0) old = atomicAdd(counter, 1u);
+    // An item leaves no tile copy in flight, only its dQ stores.
+    PrefetchQueue q{a.sched + 2, (unsigned)(a.num_seqs * a.ntiles * a.p.num_q_heads)};
+    for (int t = q.first(); q.valid(t); t = q.next((int G4_LDS*)smem_raw)) {
+      q.draw();
       dq_ds_item<D, true>(a, smem_raw, t);
-      barrier_lds();  // every wave is done with the item's LDS
-      if (threadIdx.x == 0) {
-        if (old == n - 1u) atomicExch(counter, 0u);
-        *(int G4_LDS*)smem_raw = (int)(gridDim.x + old);
-      }
-      barrier_lds();
-      t = __builtin_amdgcn_readfirstlane(*(const int G4_LDS*)smem_raw);
-      barrier_lds();  // every wave has read the slot before the next item's copies
     }
   } else {
     dq_ds_item<D, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
@@ -1783,6 +1793,13 @@ hipError_t launch_dq_roles_d(const BwdParams& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+static_assert(DqRoles256Cfg::kBM == DqDsCfg<256>::kBM,
+              "the recompute list holds stored-dS pass query tiles");
+
+__global__ void clear_counter_kernel(unsigned* c) {
+  if (threadIdx.x == 0) *c = 0u;
+}
+
 hipError_t launch_bwd_dq(const BwdParams& a, hipStream_t stream) {
   // With the dK/dV kernel's dS tiles in the workspace, dQ is a plain product.
   if (a.p.head_dim == 512) {
@@ -1791,6 +1808,13 @@ hipError_t launch_bwd_dq(const BwdParams& a, hipStream_t stream) {
   }
   if (a.p.head_dim == 256) {
     if (a.ds == nullptr) return launch_dq_roles_d<256>(a, stream);
+    if (a.dq_list != nullptr) {
+      // The list is refilled by every stored-dS pass (a fill kernel, not a
+      // memset node, so the launch sequence can be captured in a graph).
+      hipLaunchKernelGGL(clear_counter_kernel, dim3(1), dim3(64), 0, stream, a.sched + 3);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
     hipError_t e = launch_dq_ds<256>(a, stream);
     if (e != hipSuccess || a.p.vision_ids == nullptr || !a.p.bidirectional_vision) return e;
     // Query tiles with vision spans past the stored band: recomputed.

@@ -463,6 +463,34 @@ struct WorkQueue {
   }
 };
 
+// The same protocol with each ticket drawn when the previous item starts, so
+// the atomic's latency overlaps that item, and without WorkQueue's wait for
+// the item's memory operations: for items that leave no tile copy in flight
+// (their global stores do not touch LDS).
+//   PrefetchQueue q{counter, n};
+//   for (int t = q.first(); q.valid(t); t = q.next(slot)) { q.draw(); item(t); }
+struct PrefetchQueue {
+  unsigned* counter;
+  unsigned n;
+  unsigned old = 0;
+  __device__ __forceinline__ int first() const { return xcd_remap(blockIdx.x, gridDim.x); }
+  __device__ __forceinline__ bool valid(int t) const { return (unsigned)t < n; }
+  __device__ __forceinline__ void draw() {
+    if (threadIdx.x == 0) old = atomicAdd(counter, 1u);
+  }
+  __device__ __forceinline__ int next(int G4_LDS* slot) {
+    barrier_lds();  // every wave is done with the item's LDS
+    if (threadIdx.x == 0) {
+      if (old == n - 1u) atomicExch(counter, 0u);
+      *slot = (int)(gridDim.x + old);
+    }
+    barrier_lds();
+    const int t = __builtin_amdgcn_readfirstlane(*slot);
+    barrier_lds();  // every wave has read the slot before the next item's copies
+    return t;
+  }
+};
+
 // MFMA chains with A LDS operand reads in flight (kAhead unless a caller
 // picks another depth): read n + A is issued right after MFMA n and
 // sched_barrier pins that order.  Left to itself the scheduler falls back to

@@ -66,8 +66,13 @@ struct BwdParams {
   // spans reach past the stored band (set by the launcher).
   int dq_recompute_only;
   // Work-queue ticket counters of the persistent tile kernels: [0] dK/dV,
-  // [2] dQ; zeroed by the delta pass, and by each launch's last draw.
+  // [2] dQ; zeroed by the delta pass, and by each launch's last draw.  [3]
+  // counts the entries of dq_list.
   unsigned* sched;
+  // Head dim 256 with vision IDs: the query tiles the stored-dS dQ pass left
+  // for recomputation, appended by that pass ({sequence, query tile << 8 |
+  // query head}; order not significant: each entry writes its own dQ rows).
+  int2* dq_list;
 };
 
 // Workspace layout helpers (bytes).
@@ -75,6 +80,7 @@ size_t spans_bytes(const g4_problem& p);
 size_t delta_bytes(const g4_problem& p);
 size_t raise_flags_bytes(const g4_problem& p);
 constexpr size_t kSchedBytes = 256;  // work-queue counters (backward workspace tail)
+size_t dq_list_bytes(const g4_problem& p);  // after the counters
 
 // Function attributes and occupancy are per device, and one process may drive
 // several GPUs: launch-time state is cached per device (the current device,
