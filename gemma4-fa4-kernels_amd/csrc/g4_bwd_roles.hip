@@ -538,7 +538,8 @@ struct Roles256Cfg {
   static constexpr int kLdsLd = kLdsP + 4 * 4096;   // [buf][lse x 32 | delta x 32] fp32
   static constexpr int kLdsMeta = kLdsLd + 2 * 256; // [buf][vid x 32 | doc x 32] int32
   static constexpr int kLdsRed = kLdsMeta + 2 * 256;
-  static constexpr int kLdsBytes = kLdsRed + 64;
+  static constexpr int kLdsSeq = kLdsRed + 64;       // SeqTiles table (work queue)
+  static constexpr int kLdsBytes = kLdsSeq + 512;
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 };
 
@@ -734,9 +735,11 @@ struct Roles256Kernel {
   }
 };
 
-// Work item L: (KV head, sequence, key tile).
+// Work item L: (KV head, sequence, key tile); with total > 0, only the key
+// tiles that exist (total of them per KV head; the SeqTiles table is in LDS).
 template <bool META, bool QUEUE>
-__device__ __forceinline__ void dkdv_roles256_item(const BwdParams& a, char* smem_raw, int L) {
+__device__ __forceinline__ void dkdv_roles256_item(const BwdParams& a, char* smem_raw, int L,
+                                                   int total = 0) {
   using K = Roles256Kernel<META>;
   using C = Roles256Cfg;
   K ker;
@@ -751,11 +754,19 @@ __device__ __forceinline__ void dkdv_roles256_item(const BwdParams& a, char* sme
   ker.h32 = ker.lane >> 5;
 
   ker.grp = p.num_q_heads / p.num_kv_heads;
-  const int per_kvh = a.num_seqs * a.ntiles;
-  ker.kvh = L / per_kvh;
-  const int rank = L % per_kvh;
-  ker.s = rank / a.ntiles;
-  const int kt = zigzag(rank % a.ntiles, a.ntiles);
+  int kt;
+  if (total > 0) {
+    ker.kvh = L / total;
+    int local, nt;
+    SeqTiles::find_lds((const int G4_LDS*)(smem_raw + C::kLdsSeq), L % total, ker.s, local, nt);
+    kt = zigzag(local, nt);
+  } else {
+    const int per_kvh = a.num_seqs * a.ntiles;
+    ker.kvh = L / per_kvh;
+    const int rank = L % per_kvh;
+    ker.s = rank / a.ntiles;
+    kt = zigzag(rank % a.ntiles, a.ntiles);
+  }
   ker.sq = resolve_seq(p, ker.s);
   const Seq& sq = ker.sq;
   ker.j0 = kt * C::kBN;
@@ -824,12 +835,22 @@ template <bool META, bool QUEUE>
 __global__ void __launch_bounds__(Roles256Cfg::kNT, 1) dkdv_roles256_kernel(BwdParams a) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   if constexpr (QUEUE) {
-    const int n = a.num_seqs * a.ntiles * a.p.num_kv_heads;
+    int n = a.num_seqs * a.ntiles * a.p.num_kv_heads, total = 0;
+    {
+      SeqTiles tiles;
+      tiles.init(a.p.cu_seqlens_k, a.num_seqs, Roles256Cfg::kBN);
+      if (tiles.ok) {
+        total = tiles.total;
+        n = total * a.p.num_kv_heads;
+        if (threadIdx.x < 64) tiles.store((int G4_LDS*)(smem_raw + Roles256Cfg::kLdsSeq));
+      }
+      barrier_lds();
+    }
     WorkQueue wq{a.sched, n, 0};
     for (;;) {
       const int t = wq.next((int G4_LDS*)smem_raw);
       if (t >= n) break;
-      dkdv_roles256_item<META, true>(a, smem_raw, t);
+      dkdv_roles256_item<META, true>(a, smem_raw, t, total);
     }
   } else {
     dkdv_roles256_item<META, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
@@ -1578,9 +1599,12 @@ struct DqDsKernel {
 
 
 // Work item L: query tile (last, i.e. heaviest under the causal mask, first),
-// then sequence, then query head.
+// then sequence, then query head; with `tiles` (head dim 256, where the
+// band's tiles cost about the same), only existing tiles: sequence, then
+// query tile (last first), then query head.
 template <int D, bool QUEUE>
-__device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, int L) {
+__device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, int L,
+                                           const SeqTiles* tiles = nullptr) {
   using C = DqDsCfg<D>;
   DqDsKernel<D> ker;
   ker.smem = (char G4_LDS*)smem_raw;
@@ -1595,11 +1619,19 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
   const int l32 = ker.lane & 31;
 
   const int grp = p.num_q_heads / p.num_kv_heads;
-  const int per_qt = a.num_seqs * p.num_q_heads;
-  const int qt = a.ntiles - 1 - L / per_qt;
-  const int rem = L % per_qt;
-  const int s = rem / p.num_q_heads;
-  const int qh = rem % p.num_q_heads;
+  int qt, s, qh;
+  if (tiles != nullptr) {
+    int local, nt;
+    tiles->find(L / p.num_q_heads, s, local, nt);
+    qt = nt - 1 - local;
+    qh = L % p.num_q_heads;
+  } else {
+    const int per_qt = a.num_seqs * p.num_q_heads;
+    qt = a.ntiles - 1 - L / per_qt;
+    const int rem = L % per_qt;
+    s = rem / p.num_q_heads;
+    qh = rem % p.num_q_heads;
+  }
   const int kvh = qh / grp;
   ker.sq = resolve_seq(p, s);
   const Seq& sq = ker.sq;
@@ -1730,10 +1762,15 @@ __global__ void __launch_bounds__(DqDsCfg<D>::kNT, 1) dq_ds_kernel(BwdParams a) 
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   if constexpr (QUEUE) {
     // An item leaves no tile copy in flight, only its dQ stores.
-    PrefetchQueue q{a.sched + 2, (unsigned)(a.num_seqs * a.ntiles * a.p.num_q_heads)};
+    SeqTiles tiles;
+    tiles.init(a.p.cu_seqlens_q, a.num_seqs, DqDsCfg<D>::kBM);
+    const bool compact = D == 256 && tiles.ok;
+    const unsigned n = compact ? (unsigned)(tiles.total * a.p.num_q_heads)
+                               : (unsigned)(a.num_seqs * a.ntiles * a.p.num_q_heads);
+    PrefetchQueue q{a.sched + 2, n};
     for (int t = q.first(); q.valid(t); t = q.next((int G4_LDS*)smem_raw)) {
       q.draw();
-      dq_ds_item<D, true>(a, smem_raw, t);
+      dq_ds_item<D, true>(a, smem_raw, t, compact ? &tiles : nullptr);
     }
   } else {
     dq_ds_item<D, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));

@@ -463,6 +463,52 @@ struct WorkQueue {
   }
 };
 
+// Row tiles of the sequences of a packed problem, so that a launch sized by
+// its longest sequence can enumerate only the tiles that exist (in a packed
+// batch most of the (sequence, tile) grid is past its sequence's end, and
+// each such item still costs a queue draw).  Lane i of every wave holds
+// sequence i's tile count and the inclusive prefix over sequences 0..i; up to
+// 64 sequences (ok = false otherwise, and for fixed layouts).
+struct SeqTiles {
+  int cnt, incl, total;
+  bool ok;
+  __device__ __forceinline__ void init(const int* cu, int nseq, int rows_per_tile) {
+    const int lane = __lane_id();
+    ok = cu != nullptr && nseq <= 64;
+    cnt = 0;
+    if (ok && lane < nseq) cnt = (cu[lane + 1] - cu[lane] + rows_per_tile - 1) / rows_per_tile;
+    int x = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    incl = x;
+    total = __builtin_amdgcn_readfirstlane(__shfl(x, 63, 64));
+  }
+  // Sequence s, index within it and tile count of the r-th existing tile.
+  __device__ __forceinline__ void find(int r, int& s, int& local, int& nt) const {
+    s = __builtin_amdgcn_readfirstlane(__popcll(__ballot(incl <= r)));
+    local = r - __builtin_amdgcn_readfirstlane(__shfl(incl - cnt, s, 64));
+    nt = __builtin_amdgcn_readfirstlane(__shfl(cnt, s, 64));
+  }
+  // The table in LDS (64 x {incl, cnt}), for kernels that cannot keep it in
+  // registers across their items: stored by wave 0, read back by find_lds.
+  __device__ __forceinline__ void store(int G4_LDS* tab) const {
+    const int lane = __lane_id();
+    tab[2 * lane] = incl;
+    tab[2 * lane + 1] = cnt;
+  }
+  __device__ static __forceinline__ void find_lds(const int G4_LDS* tab, int r, int& s,
+                                                  int& local, int& nt) {
+    SeqTiles t;
+    const int lane = __lane_id();
+    t.incl = tab[2 * lane];
+    t.cnt = tab[2 * lane + 1];
+    t.find(r, s, local, nt);
+  }
+};
+
 // The same protocol with each ticket drawn when the previous item starts, so
 // the atomic's latency overlaps that item, and without WorkQueue's wait for
 // the item's memory operations: for items that leave no tile copy in flight
