@@ -90,22 +90,27 @@ int check_ws(const g4_problem* p, int phase, void* ws, size_t bytes) {
     if (_rc != G4_OK) return _rc; \
   } while (0)
 
-// Workspace: [spans][raise flags] (forward); backward adds [delta][dS][queue counters]
-// [dQ recompute list]
+// Workspace: [spans][raise flags][document-pass list] (forward); backward adds
+// [delta][dS][queue counters][dQ recompute list]
+size_t fwd_ws_bytes(const g4_problem& p) {
+  return align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) + g4::fwd_doc_list_bytes(p);
+}
 int* raise_flags_ptr(const g4_problem& p, void* ws) {
   return g4::raise_flags_bytes(p) ? (int*)((char*)ws + align256(g4::spans_bytes(p))) : nullptr;
 }
+unsigned* fwd_doc_list_ptr(const g4_problem& p, void* ws) {
+  if (!g4::fwd_doc_list_bytes(p)) return nullptr;
+  return (unsigned*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p));
+}
 float* delta_ptr(const g4_problem& p, void* ws) {
-  return (float*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p));
+  return (float*)((char*)ws + fwd_ws_bytes(p));
 }
 __bf16* ds_ptr(const g4_problem& p, void* ws) {
   if (!g4::ds_bytes(p)) return nullptr;
-  return (__bf16*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) +
-                   g4::delta_bytes(p));
+  return (__bf16*)((char*)ws + fwd_ws_bytes(p) + g4::delta_bytes(p));
 }
 unsigned* sched_ptr(const g4_problem& p, void* ws) {
-  return (unsigned*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) +
-                     g4::delta_bytes(p) + g4::ds_bytes(p));
+  return (unsigned*)((char*)ws + fwd_ws_bytes(p) + g4::delta_bytes(p) + g4::ds_bytes(p));
 }
 int2* dq_list_ptr(const g4_problem& p, void* ws) {
   if (!g4::dq_list_bytes(p)) return nullptr;
@@ -170,6 +175,10 @@ int fwd_impl(const g4_problem* p, const void* q, g4_layout ql, const void* k, g4
   }
   g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);
   a.raise_flags = raise_flags_ptr(*p, ws);
+  if (unsigned* dl = fwd_doc_list_ptr(*p, ws)) {
+    a.doc_list_n = dl;
+    a.doc_list = (int*)(dl + 64);
+  }
   hipError_t e = g4::launch_fwd(a, st);
   if (e != hipSuccess) return hip_fail(e, "forward");
   return G4_OK;
@@ -242,6 +251,14 @@ size_t dq_list_bytes(const g4_problem& p) {
     return 0;
   return align256((size_t)p.num_seqs * ((p.seqlen_q + 127) / 128) * p.num_q_heads * 8);
 }
+// Head dim 256 with vision and document IDs: a counter and one int per
+// (sequence, 128-query tile, query head) for the forward's second pass.
+size_t fwd_doc_list_bytes(const g4_problem& p) {
+  if (p.head_dim != 256 || p.vision_ids == nullptr || !p.bidirectional_vision ||
+      p.document_ids == nullptr)
+    return 0;
+  return 256 + align256((size_t)p.num_seqs * ((p.seqlen_q + 127) / 128) * p.num_q_heads * 4);
+}
 // One int per (sequence, 32-query group, query head) for the head-dim 512
 // forward's second pass.
 size_t raise_flags_bytes(const g4_problem& p) {
@@ -259,7 +276,7 @@ const char* g4_last_error(void) { return g_last_error.c_str(); }
 size_t g4_workspace_bytes(const g4_problem* p, int phase) {
   g_last_error.clear();
   if (check_problem(p) != G4_OK) return 0;
-  size_t b = align256(g4::spans_bytes(*p)) + g4::raise_flags_bytes(*p);
+  size_t b = fwd_ws_bytes(*p);
   if (phase == 1)
     b += g4::delta_bytes(*p) + g4::ds_bytes(*p) + g4::kSchedBytes + g4::dq_list_bytes(*p);
   return b;

@@ -275,14 +275,13 @@ struct FwdKernel {
   }
 };
 
+// One work item L of the forward (one query tile of one head).
 // FIXUP: rerun only the 32-query groups the wide kernel flagged in raise_flags.
 // OCC: workgroups per CU the register budget is sized for.
-template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, int META, bool FIXUP = false,
-          int OCC = 1>
-__global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a) {
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, int META, bool FIXUP, int OCC>
+__device__ __forceinline__ void fwd_item(const FwdParams& a, char* smem_raw, int L) {
   using K = FwdKernel<D, BN, DSPLIT, NQG, VDOUBLE, META, OCC>;
   using C = typename K::C;
-  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   K ker;
   ker.smem = (char G4_LDS*)smem_raw;
   ker.p = &a.p;
@@ -298,7 +297,6 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a
 
   // ---- work item -------------------------------------------------------
   const int grp = p.num_q_heads / p.num_kv_heads;
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int per_kvh = a.num_seqs * a.ntq * grp;
   const int kvh = L / per_kvh;
   const int rem = L % per_kvh;
@@ -356,7 +354,12 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a
         p.document_ids, sq.ktok, sq.lk, min(klo / 64 * 64, ker.a0),
         max((khi + 63) / 64 * 64, a_last_valid + 1), ker.tid, ker.lane, ker.wave,
         (int*)(smem_raw + C::kLdsRed));
-    if ((a.doc_pass == 1 && !uni) || (a.doc_pass == 2 && uni)) return;
+    if (a.doc_pass == 1 && !uni) {
+      // left to the second pass
+      if (ker.tid == 0 && a.doc_list != nullptr) a.doc_list[atomicAdd(a.doc_list_n, 1u)] = L;
+      return;
+    }
+    if (a.doc_pass == 2 && uni) return;
     if (uni) {
       ker.has_doc = false;
       ker.has_meta = ker.has_vid;
@@ -428,6 +431,29 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a
       a.lse[lse_off(p, sq, s, qh, my_i)] =
           l_tot > 0.f ? (ker.m_run + fast_log2(l_tot)) * kLn2 : kNegInf;
     }
+  }
+}
+
+template <int D, int BN, int DSPLIT, int NQG, bool VDOUBLE, int META, bool FIXUP = false,
+          int OCC = 1>
+__global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a) {
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  if constexpr (META == 3 && !FIXUP) {
+    // Second document pass with the first pass's list: the listed items,
+    // strided over a resident grid (an item leaves no tile copy in flight;
+    // the barrier retires its LDS reads).  One call site, so the item is
+    // inlined once.
+    const bool listed = a.doc_pass == 2 && a.doc_list != nullptr;
+    const int n = listed ? (int)__builtin_amdgcn_readfirstlane(*a.doc_list_n) : (int)blockIdx.x + 1;
+    for (int t = blockIdx.x; t < n; t += gridDim.x) {
+      if (t != (int)blockIdx.x) barrier_lds();
+      const int L = listed ? __builtin_amdgcn_readfirstlane(a.doc_list[t])
+                           : xcd_remap(blockIdx.x, gridDim.x);
+      fwd_item<D, BN, DSPLIT, NQG, VDOUBLE, META, FIXUP, OCC>(a, smem_raw, L);
+    }
+  } else {
+    fwd_item<D, BN, DSPLIT, NQG, VDOUBLE, META, FIXUP, OCC>(a, smem_raw,
+                                                           xcd_remap(blockIdx.x, gridDim.x));
   }
 }
 
@@ -726,10 +752,22 @@ static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fi
   FwdParams b = a;
   b.ntq = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
   b.doc_pass = doc_pass;
-  const int64_t nblocks = (int64_t)b.num_seqs * b.ntq * a.p.num_q_heads;
+  int64_t nblocks = (int64_t)b.num_seqs * b.ntq * a.p.num_q_heads;
   if (nblocks <= 0) return hipSuccess;
+  if (doc_pass == 2 && a.doc_list != nullptr) {
+    // the first pass's list, over at most one resident grid
+    static PersistentGrid grid;
+    bool many = false;
+    const int64_t g = grid.size((const void*)kern, C::kNT, C::kLdsBytes, nblocks, &many);
+    if (g <= 0) return hipErrorInvalidValue;
+    nblocks = many ? g : nblocks;
+  }
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();
+}
+
+__global__ void clear_list_kernel(unsigned* n) {
+  if (threadIdx.x == 0) *n = 0u;
 }
 
 hipError_t launch_fwd(const FwdParams& a, hipStream_t stream) {
@@ -742,6 +780,13 @@ hipError_t launch_fwd(const FwdParams& a, hipStream_t stream) {
     if (meta_kind(a.p) != 3) return launch_fwd_cfg<256, 32, 1, 4, true, 2>(a, stream);
     static_assert(FwdCfg<256, 32, 1, 4, true>::kBM == FwdCfg<256, 64, 1, 4, true>::kBM,
                   "both passes must tile queries alike");
+    if (a.doc_list_n != nullptr) {
+      // pass 1 refills the list on every call (a fill kernel, not a memset
+      // node, so the launch sequence can be captured in a graph)
+      hipLaunchKernelGGL(clear_list_kernel, dim3(1), dim3(64), 0, stream, a.doc_list_n);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
     hipError_t e = launch_fwd_cfg<256, 32, 1, 4, true, 2>(a, stream, false, /*meta=*/1,
                                                           /*doc_pass=*/1);
     if (e != hipSuccess) return e;

@@ -24,6 +24,11 @@ struct FwdParams {
   // launcher): 0 every workgroup; 1 only workgroups whose queries and visited
   // keys share one document (their document test is dropped); 2 the others.
   int doc_pass;
+  // The work items pass 1 leaves to pass 2 (appended by pass 1, in any order;
+  // doc_list_n counts them), so pass 2 runs those alone instead of testing
+  // every query tile again.  Null: pass 2 tests every tile.
+  int* doc_list;
+  unsigned* doc_list_n;
 };
 
 // Query (0..31, within its 32-query row) at position p of a dS tile's key row:
@@ -79,6 +84,7 @@ struct BwdParams {
 size_t spans_bytes(const g4_problem& p);
 size_t delta_bytes(const g4_problem& p);
 size_t raise_flags_bytes(const g4_problem& p);
+size_t fwd_doc_list_bytes(const g4_problem& p);  // counter (256 B) + entries
 constexpr size_t kSchedBytes = 256;  // work-queue counters (backward workspace tail)
 size_t dq_list_bytes(const g4_problem& p);  // after the counters
 
