@@ -421,6 +421,10 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
 __device__ __forceinline__ int zigzag(int r, int n) {
   return (r & 1) ? (r >> 1) : (n - 1 - (r >> 1));
 }
+// Its inverse: the rank of tile t among n.
+__device__ __forceinline__ int unzigzag(int t, int n) {
+  return 2 * t >= n - 1 ? 2 * (n - 1 - t) : 2 * t + 1;
+}
 
 // Thread index as seen by one work item.  In a queue kernel (QUEUE) it passes
 // through an empty asm, so the per-lane offsets derived from it are formed in

@@ -275,6 +275,62 @@ struct FwdKernel {
   }
 };
 
+// Work item L of a forward grid: heads outermost (KV head, then the grid's
+// query tiles, then the query heads of the group), query tiles sequence by
+// sequence.  A compact grid (FwdParams::compact) enumerates only the tiles
+// that exist; otherwise every sequence has ntq slots, the ones past its end
+// empty.
+struct FwdItem {
+  int kvh, qh, s, local, nt;
+  // False for an item past the last tile of a compact grid.
+  __device__ __forceinline__ bool decode(const FwdParams& a, int L, int bm) {
+    const g4_problem& p = a.p;
+    const int grp = p.num_q_heads / p.num_kv_heads;
+    SeqTiles tiles;
+    if (a.compact) tiles.init(p.cu_seqlens_q, a.num_seqs, bm);
+    const int per_kvh = (a.compact ? tiles.total : a.num_seqs * a.ntq) * grp;
+    kvh = L / per_kvh;
+    if (kvh >= p.num_kv_heads) return false;
+    const int rem = L % per_kvh;
+    const int rank = rem / grp;
+    qh = kvh * grp + rem % grp;
+    if (a.compact) {
+      tiles.find(rank, s, local, nt);
+    } else {
+      s = rank / a.ntq;
+      local = rank % a.ntq;
+      nt = a.ntq;
+    }
+    return true;
+  }
+  // The index in the full (num_seqs x ntq) grid of the item for the same
+  // query tile (the two grids order a sequence's tiles over nt and over ntq).
+  __device__ __forceinline__ int full_index(const FwdParams& a) const {
+    const int grp = a.p.num_q_heads / a.p.num_kv_heads;
+    const int r = unzigzag(zigzag(local, nt), a.ntq);
+    return (kvh * a.num_seqs * a.ntq + s * a.ntq + r) * grp + qh % grp;
+  }
+};
+
+// Workgroups of a forward grid of bm-query tiles; sets b->compact.  A packed
+// batch of 2..64 sequences enumerates only its tiles: at most
+// sum ceil(len / bm) <= (total_q + num_seqs (bm - 1)) / bm per head, against
+// num_seqs x ntq for the grid sized by the longest sequence.
+static int64_t fwd_grid(FwdParams* b, int bm, bool allow_compact) {
+  const g4_problem& p = b->p;
+  b->ntq = (p.seqlen_q + bm - 1) / bm;
+  b->compact = 0;
+  int64_t tiles = (int64_t)b->num_seqs * b->ntq;
+  if (allow_compact && p.cu_seqlens_q != nullptr && b->num_seqs > 1 && b->num_seqs <= 64) {
+    const int64_t bound = (p.total_q + (int64_t)b->num_seqs * (bm - 1)) / bm;
+    if (bound < tiles) {
+      tiles = bound;
+      b->compact = 1;
+    }
+  }
+  return tiles * p.num_q_heads;
+}
+
 // One work item L of the forward (one query tile of one head).
 // FIXUP: rerun only the 32-query groups the wide kernel flagged in raise_flags.
 // OCC: workgroups per CU the register budget is sized for.
@@ -296,14 +352,10 @@ __device__ __forceinline__ void fwd_item(const FwdParams& a, char* smem_raw, int
   const int l32 = ker.lane & 31;
 
   // ---- work item -------------------------------------------------------
-  const int grp = p.num_q_heads / p.num_kv_heads;
-  const int per_kvh = a.num_seqs * a.ntq * grp;
-  const int kvh = L / per_kvh;
-  const int rem = L % per_kvh;
-  const int rank = rem / grp;
-  const int qh = kvh * grp + rem % grp;
-  const int s = rank / a.ntq;
-  const int qt = zigzag(rank % a.ntq, a.ntq);
+  FwdItem it;
+  if (!it.decode(a, L, C::kBM)) return;
+  const int kvh = it.kvh, qh = it.qh, s = it.s;
+  const int qt = zigzag(it.local, it.nt);
 
   ker.sq = resolve_seq(p, s);
   const Seq& sq = ker.sq;
@@ -356,7 +408,9 @@ __device__ __forceinline__ void fwd_item(const FwdParams& a, char* smem_raw, int
         (int*)(smem_raw + C::kLdsRed));
     if (a.doc_pass == 1 && !uni) {
       // left to the second pass
-      if (ker.tid == 0 && a.doc_list != nullptr) a.doc_list[atomicAdd(a.doc_list_n, 1u)] = L;
+      // (its index in the full grid, which pass 2 decodes)
+      if (ker.tid == 0 && a.doc_list != nullptr)
+        a.doc_list[atomicAdd(a.doc_list_n, 1u)] = it.full_index(a);
       return;
     }
     if (a.doc_pass == 2 && uni) return;
@@ -584,15 +638,11 @@ __global__ void __launch_bounds__(256, 1) fwd_wide_kernel(FwdParams a) {
   ker.h32 = ker.lane >> 5;
   const int l32 = ker.lane & 31;
 
-  const int grp = p.num_q_heads / p.num_kv_heads;
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int per_kvh = a.num_seqs * a.ntq * grp;
-  const int kvh = L / per_kvh;
-  const int rem = L % per_kvh;
-  const int rank = rem / grp;
-  const int qh = kvh * grp + rem % grp;
-  const int s = rank / a.ntq;
-  const int qt = zigzag(rank % a.ntq, a.ntq);
+  FwdItem it;
+  if (!it.decode(a, L, C::kBM)) return;
+  const int kvh = it.kvh, qh = it.qh, s = it.s;
+  const int qt = zigzag(it.local, it.nt);
 
   ker.sq = resolve_seq(p, s);
   const Seq& sq = ker.sq;
@@ -719,8 +769,7 @@ static hipError_t launch_fwd_wide(const FwdParams& a, hipStream_t stream) {
   hipError_t e = attr.ensure((const void*)fwd_wide_kernel<D>, C::kLdsBytes);
   if (e != hipSuccess) return e;
   FwdParams b = a;
-  b.ntq = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
-  const int64_t nblocks = (int64_t)b.num_seqs * b.ntq * a.p.num_q_heads;
+  const int64_t nblocks = fwd_grid(&b, C::kBM, true);
   if (nblocks <= 0) return hipSuccess;
   hipLaunchKernelGGL(fwd_wide_kernel<D>, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes,
                      stream, b);
@@ -750,9 +799,9 @@ static hipError_t launch_fwd_cfg(const FwdParams& a, hipStream_t stream, bool fi
   hipError_t e = attr[variant].ensure((const void*)kern, C::kLdsBytes);
   if (e != hipSuccess) return e;
   FwdParams b = a;
-  b.ntq = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
   b.doc_pass = doc_pass;
-  int64_t nblocks = (int64_t)b.num_seqs * b.ntq * a.p.num_q_heads;
+  // (the fixup pass and the listed second document pass decode full-grid indices)
+  int64_t nblocks = fwd_grid(&b, C::kBM, !fixup && doc_pass != 2);
   if (nblocks <= 0) return hipSuccess;
   if (doc_pass == 2 && a.doc_list != nullptr) {
     // the first pass's list, over at most one resident grid

@@ -29,6 +29,10 @@ struct FwdParams {
   // every query tile again.  Null: pass 2 tests every tile.
   int* doc_list;
   unsigned* doc_list_n;
+  // Packed, 2..64 sequences (set by the launcher): the grid enumerates only
+  // the query tiles that exist, sequence by sequence (at most
+  // total_q / kBM + num_seqs per head), instead of num_seqs x ntq.
+  int compact;
 };
 
 // Query (0..31, within its 32-query row) at position p of a dS tile's key row:

@@ -71,6 +71,41 @@ def test_local_varlen(lq, lk, meta):
     check_forward(o, lse, o_ref, l_ref, local=True, label=f"local varlen {lq}/{lk}")
 
 
+def _many_lengths(nseq, seed, hi, extra):
+    gen = torch.Generator().manual_seed(seed)
+    lq = [int(x) for x in torch.randint(0, hi, (nseq,), generator=gen)]
+    lq[:6] = [0, 1, 127, 128, 129, 700]
+    lk = [n + int(x) for n, x in zip(lq, torch.randint(0, extra + 1, (nseq,), generator=gen))]
+    return lq, lk
+
+
+@pytest.mark.parametrize("nseq,meta", [(64, True), (65, True), (40, False)])
+def test_local_varlen_many_sequences(nseq, meta):
+    # A packed batch of 2..64 sequences runs a grid over the query tiles that
+    # exist, sequence by sequence (65 takes the grid sized by the longest
+    # sequence); with vision and document IDs the first launch lists the tiles
+    # it leaves to the second by their index in the full grid.
+    g = _g()
+    lq, lk = _many_lengths(nseq, 600 + nseq, 300, 40)
+    label = f"local varlen {nseq} sequences meta={meta}"
+    print(label, flush=True)
+    q, k, v, _, _ = qkv(nseq, sum(lq), sum(lk), 32, 16, 256)
+    vis = docs = None
+    if meta:
+        vis = vision_blocks(nseq, sum(lk), 12, 16, 400)
+        docs = torch.zeros(sum(lk), dtype=torch.int32)
+        docs[sum(lk) // 4:] = 1
+        docs[sum(lk) // 2:] = 2
+    cq, ck = cu(lq), cu(lk)
+    o, lse = g.fa4_local_varlen_forward(
+        q.to(DEV), k.to(DEV), v.to(DEV), cq.to(DEV), ck.to(DEV),
+        max_seqlen_q=max(lq), max_seqlen_k=max(lk),
+        vision_block_ids=None if vis is None else vis.to(DEV),
+        document_ids=None if docs is None else docs.to(DEV))
+    o_ref, l_ref, *_ = oracle_fwd_bwd(q, k, v, cq, ck, window=1024, vision=vis, docs=docs)
+    check_forward(o, lse, o_ref, l_ref, local=True, label=label)
+
+
 @pytest.mark.parametrize("s", [1, 31, 32, 33, 63, 64, 65, 127, 128, 129, 511, 512, 513, 1000,
                                1024, 2048])
 def test_global_text_fixed(s):
@@ -108,6 +143,23 @@ def test_global_varlen(lq, lk):
                                                   max_seqlen_k=max(lk))
     o_ref, l_ref, *_ = oracle_fwd_bwd(q, k, v, cq, ck, window=None)
     check_forward(o, lse, o_ref, l_ref, local=False, label=f"global varlen {lq}")
+
+
+@pytest.mark.parametrize("nseq", [64, 65])
+def test_global_varlen_many_sequences(nseq):
+    # the head-dim 512 fast pass over the tiles that exist (64 sequences) or
+    # the full grid (65), then the rescaling pass over the flagged groups
+    g = _g()
+    lq, lk = _many_lengths(nseq, 700 + nseq, 200, 30)
+    print(f"global varlen {nseq} sequences", flush=True)
+    q, k, v, _, _ = qkv(800 + nseq, sum(lq), sum(lk), 32, 4, 512, unit_logits=False)
+    cq, ck = cu(lq), cu(lk)
+    with torch.no_grad():
+        o, lse = g.fa4_global_varlen_forward_only(q.to(DEV), k.to(DEV), v.to(DEV), cq.to(DEV),
+                                                  ck.to(DEV), max_seqlen_q=max(lq),
+                                                  max_seqlen_k=max(lk))
+    o_ref, l_ref, *_ = oracle_fwd_bwd(q, k, v, cq, ck, window=None)
+    check_forward(o, lse, o_ref, l_ref, local=False, label=f"global varlen {nseq} sequences")
 
 
 def test_forward_is_bitwise_repeatable_on_a_side_stream():
