@@ -107,7 +107,8 @@ struct RolesCfg {
   static constexpr int kLdsLd = kLdsXp + 4 * 4 * 1024;  // [buf][lse x 32 | delta x 32] fp32
   static constexpr int kLdsMeta = kLdsLd + 2 * 256;     // [buf][vid x 32 | doc x 32] int32
   static constexpr int kLdsRed = kLdsMeta + 2 * 256;
-  static constexpr int kLdsBytes = kLdsRed + 64;
+  static constexpr int kLdsSeq = kLdsRed + 64;  // SeqUnitsByLength table (work queue)
+  static constexpr int kLdsBytes = kLdsSeq + 512;
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 };
 
@@ -464,15 +465,29 @@ __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_r
 // tile's query count falls linearly with its index, so a pair carries about
 // the same number of steps whatever r is.  KV head slowest keeps the
 // workgroups of one XCD on one head group's Q and dO.
+// With `by_length` (the queue launch of a packed batch of up to 64
+// sequences): only the pairs that exist, sequence by sequence from the longest
+// (a pair's cost grows with its sequence's length, and a longer sequence has
+// more pairs: the heaviest items go first), then KV head, then pair.
 template <bool META, bool QUEUE>
-__device__ __forceinline__ void dkdv_roles_pair(const BwdParams& a, char* smem_raw, int L) {
+__device__ __forceinline__ void dkdv_roles_pair(const BwdParams& a, char* smem_raw, int L,
+                                                bool by_length = false) {
   using C = RolesCfg;
-  const int npairs = (a.ntiles + 1) / 2;
-  const int per_kvh = npairs * a.num_seqs;
-  const int kvh = L / per_kvh;
-  const int rem = L % per_kvh;
-  const int r = npairs - 1 - rem / a.num_seqs;
-  const int s = rem % a.num_seqs;
+  int kvh, r, s;
+  if (by_length) {
+    int local, n;
+    SeqUnitsByLength::find_lds((const int G4_LDS*)(smem_raw + C::kLdsSeq), L, s, local, n);
+    const int np = n / a.p.num_kv_heads;
+    kvh = local / np;
+    r = local % np;
+  } else {
+    const int npairs = (a.ntiles + 1) / 2;
+    const int per_kvh = npairs * a.num_seqs;
+    kvh = L / per_kvh;
+    const int rem = L % per_kvh;
+    r = npairs - 1 - rem / a.num_seqs;
+    s = rem % a.num_seqs;
+  }
   const Seq sq = resolve_seq(a.p, s);
   const int nt = (sq.lk + C::kBN - 1) / C::kBN;
   if (r >= (nt + 1) / 2) return;
@@ -494,12 +509,25 @@ template <bool META, bool QUEUE>
 __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams a) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   if constexpr (QUEUE) {
-    const int n = (a.ntiles + 1) / 2 * a.num_seqs * a.p.num_kv_heads;
+    using C = RolesCfg;
+    const int hkv = a.p.num_kv_heads;
+    int n = (a.ntiles + 1) / 2 * a.num_seqs * hkv;
+    const bool by_length = a.p.cu_seqlens_q != nullptr && a.p.cu_seqlens_k != nullptr &&
+                           a.num_seqs <= 64;
+    if (by_length) {
+      // ordered by query length; units: pairs of key tiles over all KV heads
+      SeqUnitsByLength order;
+      order.init(a.p.cu_seqlens_q, a.p.cu_seqlens_k, a.num_seqs,
+                 [&](int lk) { return ((lk + C::kBN - 1) / C::kBN + 1) / 2 * hkv; });
+      n = order.total;
+      if (threadIdx.x < 64) order.store((int G4_LDS*)(smem_raw + C::kLdsSeq));
+      barrier_lds();
+    }
     WorkQueue wq{a.sched, n, 0};
     for (;;) {
       const int t = wq.next((int G4_LDS*)smem_raw);
       if (t >= n) break;
-      dkdv_roles_pair<META, true>(a, smem_raw, t);
+      dkdv_roles_pair<META, true>(a, smem_raw, t, by_length);
     }
   } else {
     dkdv_roles_pair<META, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));

@@ -513,6 +513,60 @@ struct SeqTiles {
   }
 };
 
+// Work units of the sequences of a packed problem (up to 64) in the order of
+// their query lengths, longest first (ties by index): for a queue whose items
+// all cost about the same within a sequence and whose cost grows with the
+// sequence's length, so the heaviest items are drawn first.  Lane i of every
+// wave holds sequence i's unit count and the units of the sequences before it
+// in that order.
+struct SeqUnitsByLength {
+  int cnt, lo, total;
+  // cu_len orders the sequences; units(length from cu_cnt) counts their units.
+  template <class Units>
+  __device__ __forceinline__ void init(const int* cu_len, const int* cu_cnt, int nseq,
+                                       Units units) {
+    const int lane = __lane_id();
+    int len = -1;
+    cnt = 0;
+    if (lane < nseq) {
+      len = cu_len[lane + 1] - cu_len[lane];
+      cnt = units(cu_cnt[lane + 1] - cu_cnt[lane]);
+    }
+    int before = 0;
+    for (int j = 0; j < nseq; ++j) {
+      const int lj = __builtin_amdgcn_readlane(len, j);
+      const int cj = __builtin_amdgcn_readlane(cnt, j);
+      if (lj > len || (lj == len && j < lane)) before += cj;
+    }
+    lo = before;
+    int x = cnt;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+    total = __builtin_amdgcn_readfirstlane(x);
+  }
+  // Sequence s, its unit count n and the index within it of unit u (< total).
+  __device__ __forceinline__ void find(int u, int& s, int& local, int& n) const {
+    const unsigned long long m = __ballot(lo <= u && u < lo + cnt);
+    s = __builtin_amdgcn_readfirstlane(__ffsll((long long)m) - 1);
+    local = u - __builtin_amdgcn_readfirstlane(__shfl(lo, s, 64));
+    n = __builtin_amdgcn_readfirstlane(__shfl(cnt, s, 64));
+  }
+  // The table in LDS (64 x {lo, cnt}): stored by wave 0, read back by find_lds.
+  __device__ __forceinline__ void store(int G4_LDS* tab) const {
+    const int lane = __lane_id();
+    tab[2 * lane] = lo;
+    tab[2 * lane + 1] = cnt;
+  }
+  __device__ static __forceinline__ void find_lds(const int G4_LDS* tab, int u, int& s,
+                                                  int& local, int& n) {
+    SeqUnitsByLength t;
+    const int lane = __lane_id();
+    t.lo = tab[2 * lane];
+    t.cnt = tab[2 * lane + 1];
+    t.find(u, s, local, n);
+  }
+};
+
 // The same protocol with each ticket drawn when the previous item starts, so
 // the atomic's latency overlaps that item, and without WorkQueue's wait for
 // the item's memory operations: for items that leave no tile copy in flight
