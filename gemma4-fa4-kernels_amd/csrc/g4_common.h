@@ -416,6 +416,21 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   return xcd * base + min(xcd, extra) + pos;
 }
 
+// xcd_remap for a grid whose work items come in zigzag ranks (unit items per
+// rank, see zigzag): within each XCD's run the even ranks (heavy tiles,
+// heaviest first) come before the odd ranks taken backwards (light tiles,
+// heaviest first), so each XCD starts its heaviest items first and ends on
+// its lightest.  Needs nblocks to be a multiple of 16 unit (every run then
+// holds an even number of whole ranks).
+__device__ __forceinline__ int xcd_remap_desc(int bid, int nblocks, int unit) {
+  constexpr int kXcd = 8;
+  const int xcd = bid % kXcd, pos = bid / kXcd;
+  const int len = nblocks / kXcd, m = len / (2 * unit);
+  const int q = pos / unit, g = pos % unit;
+  const int r = q < m ? 2 * q : 4 * m - 1 - 2 * q;
+  return xcd * len + r * unit + g;
+}
+
 // Tile rank -> tile index alternating from the heaviest (last) tile:
 // n-1, 0, n-2, 1, ...
 __device__ __forceinline__ int zigzag(int r, int n) {

@@ -303,6 +303,12 @@ struct FwdItem {
     }
     return true;
   }
+  // The item of this workgroup in a launch of one item per workgroup.
+  __device__ static __forceinline__ int of_block(const FwdParams& a) {
+    return a.desc_order ? xcd_remap_desc(blockIdx.x, gridDim.x,
+                                          a.p.num_q_heads / a.p.num_kv_heads)
+                        : xcd_remap(blockIdx.x, gridDim.x);
+  }
   // The index in the full (num_seqs x ntq) grid of the item for the same
   // query tile (the two grids order a sequence's tiles over nt and over ntq).
   __device__ __forceinline__ int full_index(const FwdParams& a) const {
@@ -320,6 +326,7 @@ static int64_t fwd_grid(FwdParams* b, int bm, bool allow_compact) {
   const g4_problem& p = b->p;
   b->ntq = (p.seqlen_q + bm - 1) / bm;
   b->compact = 0;
+  b->desc_order = 0;
   int64_t tiles = (int64_t)b->num_seqs * b->ntq;
   if (allow_compact && p.cu_seqlens_q != nullptr && b->num_seqs > 1 && b->num_seqs <= 64) {
     const int64_t bound = (p.total_q + (int64_t)b->num_seqs * (bm - 1)) / bm;
@@ -328,7 +335,12 @@ static int64_t fwd_grid(FwdParams* b, int bm, bool allow_compact) {
       b->compact = 1;
     }
   }
-  return tiles * p.num_q_heads;
+  const int64_t n = tiles * p.num_q_heads;
+  // Heaviest first within each XCD: the zigzag ranks of a sequence alternate
+  // heavy and light only if ntq is even (rank parity = tile-rank parity).
+  const int grp = p.num_q_heads / p.num_kv_heads;
+  if (allow_compact && !b->compact && b->ntq % 2 == 0 && n % (16 * grp) == 0) b->desc_order = 1;
+  return n;
 }
 
 // One work item L of the forward (one query tile of one head).
@@ -502,12 +514,11 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a
     for (int t = blockIdx.x; t < n; t += gridDim.x) {
       if (t != (int)blockIdx.x) barrier_lds();
       const int L = listed ? __builtin_amdgcn_readfirstlane(a.doc_list[t])
-                           : xcd_remap(blockIdx.x, gridDim.x);
+                           : FwdItem::of_block(a);
       fwd_item<D, BN, DSPLIT, NQG, VDOUBLE, META, FIXUP, OCC>(a, smem_raw, L);
     }
   } else {
-    fwd_item<D, BN, DSPLIT, NQG, VDOUBLE, META, FIXUP, OCC>(a, smem_raw,
-                                                           xcd_remap(blockIdx.x, gridDim.x));
+    fwd_item<D, BN, DSPLIT, NQG, VDOUBLE, META, FIXUP, OCC>(a, smem_raw, FwdItem::of_block(a));
   }
 }
 
@@ -638,7 +649,7 @@ __global__ void __launch_bounds__(256, 1) fwd_wide_kernel(FwdParams a) {
   ker.h32 = ker.lane >> 5;
   const int l32 = ker.lane & 31;
 
-  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int L = FwdItem::of_block(a);
   FwdItem it;
   if (!it.decode(a, L, C::kBM)) return;
   const int kvh = it.kvh, qh = it.qh, s = it.s;

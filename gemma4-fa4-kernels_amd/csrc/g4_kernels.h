@@ -33,6 +33,9 @@ struct FwdParams {
   // the query tiles that exist, sequence by sequence (at most
   // total_q / kBM + num_seqs per head), instead of num_seqs x ntq.
   int compact;
+  // Full grid whose XCD runs hold whole rank pairs (set by the launcher):
+  // blocks map onto items heaviest first within each XCD (xcd_remap_desc).
+  int desc_order;
 };
 
 // Query (0..31, within its 32-query row) at position p of a dS tile's key row:
