@@ -610,13 +610,14 @@ struct Roles256Kernel {
     qcp.issue_clamped(qb, a->ql.token_stride, min(C::kBM, sq.lq - i0),
                       smem + C::kLdsQ + buf * C::kTile);
     const int i = min(i0 + (lane & 31), sq.lq - 1);
-    if (wave == 0) {
+    // (row data by the first two waves of the issuing role)
+    if ((wave & 3) == 0) {
       char G4_LDS* dst = smem + C::kLdsLd + buf * 256;
       if (lane < 32)
         g2l4(a->lse + lse_off(a->p, sq, s, qh, i), dst);
       else
         g2l4(a->delta + (int64_t)qh * tq + sq.qtok + i, dst);
-    } else if (wave == 1 && has_meta) {
+    } else if ((wave & 3) == 1 && has_meta) {
       char G4_LDS* dst = smem + C::kLdsMeta + buf * 256;
       const int64_t kidx = sq.ktok + i + off;
       if (lane < 32) {
@@ -640,7 +641,6 @@ struct Roles256Kernel {
     const char G4_LDS* dot = smem + C::kLdsDo + cur * C::kTile;
     __builtin_amdgcn_sched_barrier(0);
     f32x16 sv = f32x16{};
-    if (it + 1 < nsteps) issue_q(it + 1, cur ^ 1);
     row_steps<C::kNC, C::kReads>(rrd, qt, sv, frag);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -680,6 +680,9 @@ struct Roles256Kernel {
     }
     barrier_lds();  // B2
 
+    // The next step's Q after the softmax (on the step's critical path) and
+    // before the dV MFMAs (these waves then wait at B1 for the dS waves).
+    if (it + 1 < nsteps) issue_q(it + 1, cur ^ 1);
     __builtin_amdgcn_sched_barrier(0);
     acc_steps<C::kNB, C::kReads>(trd, dot, pb, acc);
     __builtin_amdgcn_sched_barrier(0);
