@@ -129,7 +129,8 @@ struct RolesKernel {
   uint32_t ds_lane;  // byte offset of this lane's dS run inside a tile
   RowReader<C::kCPR> rrd;
   TrReader<C::kCPR> trd;
-  TileCopier<C::kCPR, C::kBM, 4> qcp, docp;  // Q by the P waves, dO by the dS waves
+  TileCopier<C::kCPR, C::kBM, 8> qcp;  // Q: half by the P waves, half by the dS waves
+  TileCopier<C::kCPR, C::kBM, 4> docp;  // dO by the dS waves
   bf16x8 frag[C::kNC];   // K (P waves) or V (dS waves), B operands
   f32x16 acc[C::kNB];    // dV^T (P waves) or dK^T (dS waves)
 
@@ -149,15 +150,21 @@ struct RolesKernel {
     docp.issue_clamped(db, a->dol.token_stride, min(C::kBM, sq.lq - i0),
                        smem + C::kLdsDo + buf * C::kTile);
   }
-  // Q tile and, by waves 0 and 1, the row data: LSE (lanes 0-31) and delta
-  // (lanes 32-63) of the 32 rows; with metadata the vision / document IDs of
-  // the rows' K positions.
-  __device__ __forceinline__ void issue_q(int it, int buf) {
+  // This wave's half of the Q tile's rows (every wave issues one).
+  __device__ __forceinline__ void issue_q_rows(int it, int buf) {
     int qh, i0;
     coords(it, qh, i0);
     const __bf16* qb = a->q + tok_off(sq, s, sq.qtok, i0, a->ql) + (int64_t)qh * a->ql.head_stride;
     qcp.issue_clamped(qb, a->ql.token_stride, min(C::kBM, sq.lq - i0),
                       smem + C::kLdsQ + buf * C::kTile);
+  }
+  // The P waves' rows of the Q tile and, by waves 0 and 1, the row data: LSE
+  // (lanes 0-31) and delta (lanes 32-63) of the 32 rows; with metadata the
+  // vision / document IDs of the rows' K positions.
+  __device__ __forceinline__ void issue_q(int it, int buf) {
+    int qh, i0;
+    coords(it, qh, i0);
+    issue_q_rows(it, buf);
     const int i = min(i0 + (lane & 31), sq.lq - 1);
     if (wave == 0) {
       char G4_LDS* dst = smem + C::kLdsLd + buf * 256;
@@ -280,6 +287,9 @@ struct RolesKernel {
     for (int q4 = 0; q4 < 4; ++q4)
       *(f32x4 G4_LDS*)(xp + ((slot * 4 + q4) * 64 + lane) * 16) =
           f32x4{dp[4 * q4], dp[4 * q4 + 1], dp[4 * q4 + 2], dp[4 * q4 + 3]};
+    // Half of the next Q tile (these waves wait at B2 for the P waves' S
+    // partial, which the other half's issue delays).
+    if (it + 1 < nsteps) issue_q_rows(it + 1, cur ^ 1);
     barrier_lds();  // B2
 
     // dP = (slice 0 partial) + (slice 1 partial) in both waves of the pair.
@@ -444,13 +454,15 @@ __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_r
   // partial in accumulator registers 0-7.
   if (!QUEUE && pwave && ker.dh) ker.rrd.base ^= 16 * C::kCPR * 16;
   ker.trd.init(ker.lane, ker.dh * C::kDH * 2);
-  ker.qcp.init(a.ql.token_stride, ker.wave & 3, ker.lane);
+  ker.qcp.init(a.ql.token_stride, ker.wave, ker.lane);
   ker.docp.init(a.dol.token_stride, ker.wave & 3, ker.lane);
   if (nsteps > 0) {
-    if (pwave)
+    if (pwave) {
       ker.issue_q(0, 0);
-    else
+    } else {
       ker.issue_do(0, 0);
+      ker.issue_q_rows(0, 0);
+    }
   }
   // Both roles run nsteps steps of three barriers each.
   if (pwave)
