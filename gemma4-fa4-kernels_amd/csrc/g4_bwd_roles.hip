@@ -166,19 +166,23 @@ struct RolesKernel {
     coords(it, qh, i0);
     issue_q_rows(it, buf);
     const int i = min(i0 + (lane & 31), sq.lq - 1);
+    // uniform bases at the tile's first (clamped) row, per-lane offsets of
+    // at most 31 rows
+    const int i0c = min(i0, sq.lq - 1);
+    const uint32_t ioff = (uint32_t)(i - i0c) * 4u;
     if (wave == 0) {
       char G4_LDS* dst = smem + C::kLdsLd + buf * 256;
       if (lane < 32)
-        g2l4(a->lse + lse_off(a->p, sq, s, qh, i), dst);
+        b2l4(a->lse + lse_off(a->p, sq, s, qh, i0c), ioff, dst);
       else
-        g2l4(a->delta + (int64_t)qh * tq + sq.qtok + i, dst);
+        b2l4(a->delta + (int64_t)qh * tq + sq.qtok + i0c, ioff, dst);
     } else if (wave == 1 && has_meta) {
       char G4_LDS* dst = smem + C::kLdsMeta + buf * 256;
-      const int64_t kidx = sq.ktok + i + off;
+      const int64_t k0 = sq.ktok + i0c + off;
       if (lane < 32) {
-        if (has_vid) g2l4(a->p.vision_ids + kidx, dst);
+        if (has_vid) b2l4(a->p.vision_ids + k0, ioff, dst);
       } else {
-        if (has_doc) g2l4(a->p.document_ids + kidx, dst);
+        if (has_doc) b2l4(a->p.document_ids + k0, ioff, dst);
       }
     }
   }
@@ -623,19 +627,23 @@ struct Roles256Kernel {
                       smem + C::kLdsQ + buf * C::kTile);
     const int i = min(i0 + (lane & 31), sq.lq - 1);
     // (row data by the first two waves of the issuing role)
+    // uniform bases at the tile's first (clamped) row, per-lane offsets of
+    // at most 31 rows
+    const int i0c = min(i0, sq.lq - 1);
+    const uint32_t ioff = (uint32_t)(i - i0c) * 4u;
     if ((wave & 3) == 0) {
       char G4_LDS* dst = smem + C::kLdsLd + buf * 256;
       if (lane < 32)
-        g2l4(a->lse + lse_off(a->p, sq, s, qh, i), dst);
+        b2l4(a->lse + lse_off(a->p, sq, s, qh, i0c), ioff, dst);
       else
-        g2l4(a->delta + (int64_t)qh * tq + sq.qtok + i, dst);
+        b2l4(a->delta + (int64_t)qh * tq + sq.qtok + i0c, ioff, dst);
     } else if ((wave & 3) == 1 && has_meta) {
       char G4_LDS* dst = smem + C::kLdsMeta + buf * 256;
-      const int64_t kidx = sq.ktok + i + off;
+      const int64_t k0 = sq.ktok + i0c + off;
       if (lane < 32) {
-        if (has_vid) g2l4(a->p.vision_ids + kidx, dst);
+        if (has_vid) b2l4(a->p.vision_ids + k0, ioff, dst);
       } else {
-        if (has_doc) g2l4(a->p.document_ids + kidx, dst);
+        if (has_doc) b2l4(a->p.document_ids + k0, ioff, dst);
       }
     }
   }

@@ -126,9 +126,15 @@ __device__ __forceinline__ void b2l16(const void* base, uint32_t voff, char G4_L
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (void G4_LDS*)lds_wave_base, 16, voff, 0, 0, 0);
 }
 
-// Async 4-byte global -> LDS copy: lane l writes LDS bytes [base + 4 l, +4).
-__device__ __forceinline__ void g2l4(const void* gptr, char G4_LDS* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(gptr, (void G4_LDS*)lds_wave_base, 4, 0, 0);
+// Async 4-byte global -> LDS copy: lane l writes LDS bytes [lds_wave_base +
+// 4 l, +4) from base + voff (a uniform base, a 32-bit per-lane byte offset).
+// Through a buffer descriptor rather than a global address: the compiler
+// counts a buffer copy with the vector memory counter only, while after the
+// global form the LDS operand reads that follow were all waited for at once.
+__device__ __forceinline__ void b2l4(const void* base, uint32_t voff, char G4_LDS* lds_wave_base) {
+  __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (void G4_LDS*)lds_wave_base, 4, voff, 0, 0, 0);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -352,9 +358,12 @@ __device__ __forceinline__ bool doc_uniform(const int* doc, int64_t ktok, int lk
 // [vid x 64 | doc x 64] int32 at dst.  One wave issues it.
 __device__ __forceinline__ void issue_key_meta(const g4_problem& p, const Seq& sq, int j0,
                                                char G4_LDS* dst, int lane, bool vid, bool doc) {
-  const int64_t idx = sq.ktok + min(j0 + lane, sq.lk - 1);
-  if (vid) g2l4(p.vision_ids + idx, dst);
-  if (doc) g2l4(p.document_ids + idx, dst + 256);
+  // uniform base at the tile's first (clamped) key, small per-lane offsets
+  const int j0c = min(j0, sq.lk - 1);
+  const int64_t base = sq.ktok + j0c;
+  const uint32_t off = (uint32_t)(min(j0 + lane, sq.lk - 1) - j0c) * 4u;
+  if (vid) b2l4(p.vision_ids + base, off, dst);
+  if (doc) b2l4(p.document_ids + base, off, dst + 256);
 }
 
 // First key tile (64 keys) of the stored-dS band of the 32-query row whose

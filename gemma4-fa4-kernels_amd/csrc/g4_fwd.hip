@@ -42,9 +42,12 @@ struct FwdCfg {
 // (clamped to its last key; keys past the end are masked by index).
 __device__ __forceinline__ void issue_meta(const g4_problem& p, const Seq& sq, int j0,
                                            char G4_LDS* dst, int lane, bool vid, bool doc) {
-  const int64_t idx = sq.ktok + min(j0 + lane, sq.lk - 1);
-  if (vid) g2l4(p.vision_ids + idx, dst);
-  if (doc) g2l4(p.document_ids + idx, dst + 256);
+  // uniform base at the tile's first (clamped) key, small per-lane offsets
+  const int j0c = min(j0, sq.lk - 1);
+  const int64_t base = sq.ktok + j0c;
+  const uint32_t off = (uint32_t)(min(j0 + lane, sq.lk - 1) - j0c) * 4u;
+  if (vid) b2l4(p.vision_ids + base, off, dst);
+  if (doc) b2l4(p.document_ids + base, off, dst + 256);
 }
 
 // Largest score excess (log2 units) over a row's running maximum that the
