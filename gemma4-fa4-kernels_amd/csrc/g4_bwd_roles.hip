@@ -1580,7 +1580,7 @@ struct DqDsKernel {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const int chunk = (wave & 1) * 2 + c;
-        g2l16(src + chunk * 1024 + lane * 16, dst + chunk * 1024);
+        b2l16(src, (uint32_t)(chunk * 1024 + lane * 16), dst + chunk * 1024);
       }
     }
   }
@@ -1754,7 +1754,8 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
     const char G4_LDS* ds0 = ker.smem + C::kLdsDs + (cur * 4 + g0) * 4096;
     const char G4_LDS* ds1 = ds0 + 4096;
     const bool v0 = kt >= ker.lo0 && kt <= ker.hi0, v1 = kt >= ker.lo1 && kt <= ker.hi1;
-    // (The band kernel measured slower pipelined: 5.52 vs 5.39 ms on config 5.)
+    // (The band kernel measured slower pipelined: 5.52 vs 5.39 ms on config 5;
+    // with its dS copies through buffer descriptors, the same: 3.97 ms both.)
     if (!kBand && v0 && v1) {
       ker.ktile_both(ktile, ds0, ds1);
     } else {

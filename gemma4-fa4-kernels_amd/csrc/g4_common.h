@@ -83,11 +83,6 @@ __device__ __forceinline__ bf16x8 cat4(bf16x4 a, bf16x4 b) {
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// Async 16-byte global -> LDS copy: lane l writes LDS bytes [base + 16 l, +16).
-__device__ __forceinline__ void g2l16(const void* gptr, char G4_LDS* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(gptr, (void G4_LDS*)lds_wave_base, 16, 0, 0);
-}
-
 __device__ __forceinline__ bf16x8 ld_global16(const void* p) {
   return *(const bf16x8*)p;
 }
@@ -242,7 +237,7 @@ struct TileCopier {
         const int r = u * kRows + lr;
         const uint32_t c = lc ^ (((r & 3) << 2) | ((r >> 2) & 3));
         const char* row = g + (int64_t)(u * kRows) * stride_bytes;
-        g2l16(row + c * 16u, tile + u * 1024);
+        b2l16(row, c * 16u, tile + u * 1024);
       }
     } else {
       // Two rows per instruction: lane row lr = ln >> 5, row r = 2u + lr.  As 2u
