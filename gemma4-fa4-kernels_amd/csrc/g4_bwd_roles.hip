@@ -1491,9 +1491,13 @@ struct DqDsCfg {
   static constexpr int kBN = 64;   // keys per tile
   static constexpr int kCPR = D / 8;
   static constexpr int kKTile = kBN * D * 2;
+  // Query heads per item: at head dim 256 the two heads of a GQA pair share
+  // the item's K tiles (halving K copies per query); the register file has
+  // room for both heads' dQ only there.
+  static constexpr int kHeads = D == 256 ? 2 : 1;
   static constexpr int kLdsK = 0;                    // [2 buf] K tiles
-  static constexpr int kLdsDs = 2 * kKTile;          // [2 buf][4 rows] dS tiles
-  static constexpr int kLdsBytes = kLdsDs + 2 * 4 * 4096;
+  static constexpr int kLdsDs = 2 * kKTile;          // [2 buf][kHeads][4 rows] dS tiles
+  static constexpr int kLdsBytes = kLdsDs + 2 * kHeads * 4 * 4096;
   static constexpr int kDW = D / 4;      // head dims per wave
   static constexpr int kNBw = kDW / 32;  // 32-wide head-dim blocks per wave
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
@@ -1563,31 +1567,39 @@ struct DqDsKernel {
   int64_t kstride;
   const char* ds_copy_row;  // dS tile of key tile lo_copy in the copied row
   int64_t ds_col_stride;
+  int64_t ds_head_stride;  // bytes from one query head's dS tiles to the next's
+  int nh;                  // query heads of this item (1 or C::kHeads)
   BlockTrReader<C::kCPR, C::kNBw> trk;
   PlainTrReader trs;
   TileCopier<C::kCPR, C::kBN, C::kNW> kcp;
-  f32x16 acc[2][C::kNBw];
+  f32x16 acc[C::kHeads][2][C::kNBw];
 
   __device__ __forceinline__ void issue(int kt, int buf) {
     const int row0 = kt * C::kBN;
     kcp.issue_clamped(kbase + row0 * kstride, kstride, min(C::kBN, sq.lk - row0),
                       smem + C::kLdsK + buf * C::kKTile);
-    // dS: four 4 KB tiles, two 1 KB chunks per wave.
+    // dS: four 4 KB tiles per head, two 1 KB chunks per wave and head.
     const int g = wave >> 1;
     if (kt >= lo_copy && kt <= hi_copy) {
       const char* src = ds_copy_row + (int64_t)(kt - lo_copy) * ds_col_stride;
-      char G4_LDS* dst = smem + C::kLdsDs + (buf * 4 + g) * 4096;
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int chunk = (wave & 1) * 2 + c;
-        b2l16(src, (uint32_t)(chunk * 1024 + lane * 16), dst + chunk * 1024);
+      for (int h = 0; h < C::kHeads; ++h) {
+        if (h < nh) {
+          char G4_LDS* dst = smem + C::kLdsDs + ((buf * C::kHeads + h) * 4 + g) * 4096;
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const int chunk = (wave & 1) * 2 + c;
+            b2l16(src + h * ds_head_stride, (uint32_t)(chunk * 1024 + lane * 16),
+                  dst + chunk * 1024);
+          }
+        }
       }
     }
   }
 
   template <int KS>
-  __device__ __forceinline__ void kstep(const char G4_LDS* kt_tile, const char G4_LDS* ds0,
-                                        const char G4_LDS* ds1, bool v0, bool v1) {
+  __device__ __forceinline__ void kstep(const char G4_LDS* kt_tile, const char G4_LDS* dsb,
+                                        bool v0, bool v1) {
     bf16x8 ak[C::kNBw];
     ak[0] = trk.template read<16 * KS, 0>(kt_tile);
     ak[1] = trk.template read<16 * KS, 1>(kt_tile);
@@ -1595,15 +1607,20 @@ struct DqDsKernel {
       ak[2] = trk.template read<16 * KS, 2>(kt_tile);
       ak[3] = trk.template read<16 * KS, 3>(kt_tile);
     }
-    if (v0) {
-      const bf16x8 bs = trs.template read<16 * KS>(ds0);
 #pragma unroll
-      for (int b = 0; b < C::kNBw; ++b) acc[0][b] = mfma32(ak[b], bs, acc[0][b]);
-    }
-    if (v1) {
-      const bf16x8 bs = trs.template read<16 * KS>(ds1);
+    for (int h = 0; h < C::kHeads; ++h) {
+      if (h >= nh) break;
+      const char G4_LDS* ds0 = dsb + h * 4 * 4096;
+      if (v0) {
+        const bf16x8 bs = trs.template read<16 * KS>(ds0);
 #pragma unroll
-      for (int b = 0; b < C::kNBw; ++b) acc[1][b] = mfma32(ak[b], bs, acc[1][b]);
+        for (int b = 0; b < C::kNBw; ++b) acc[h][0][b] = mfma32(ak[b], bs, acc[h][0][b]);
+      }
+      if (v1) {
+        const bf16x8 bs = trs.template read<16 * KS>(ds0 + 4096);
+#pragma unroll
+        for (int b = 0; b < C::kNBw; ++b) acc[h][1][b] = mfma32(ak[b], bs, acc[h][1][b]);
+      }
     }
   }
 
@@ -1633,7 +1650,7 @@ struct DqDsKernel {
       for (int g = 0; g < 2; ++g)
 #pragma unroll
         for (int b = 0; b < C::kNBw; ++b)
-          acc[g][b] = mfma32(ak[KS & 1][b], bs[KS & 1][g], acc[g][b]);
+          acc[0][g][b] = mfma32(ak[KS & 1][b], bs[KS & 1][g], acc[0][g][b]);
       __builtin_amdgcn_sched_barrier(0);
       kpipe<KS + 1>(kt_tile, ds0, ds1, ak, bs);
     }
@@ -1649,10 +1666,19 @@ struct DqDsKernel {
 };
 
 
+// Query heads of one dQ-from-dS item: the GQA pair at head dim 256 (both
+// share their KV head's K tiles), one otherwise.
+template <int D>
+__host__ __device__ __forceinline__ int dq_ds_heads(const g4_problem& p) {
+  return DqDsCfg<D>::kHeads > 1 && p.num_q_heads / p.num_kv_heads >= DqDsCfg<D>::kHeads
+             ? DqDsCfg<D>::kHeads
+             : 1;
+}
+
 // Work item L: query tile (last, i.e. heaviest under the causal mask, first),
-// then sequence, then query head; with `tiles` (head dim 256, where the
-// band's tiles cost about the same), only existing tiles: sequence, then
-// query tile (last first), then query head.
+// then sequence, then query head (or GQA head pair, dq_ds_heads); with
+// `tiles` (head dim 256, where the band's tiles cost about the same), only
+// existing tiles: sequence, then query tile (last first), then head (pair).
 template <int D, bool QUEUE>
 __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, int L,
                                            const SeqTiles* tiles = nullptr) {
@@ -1670,18 +1696,21 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
   const int l32 = ker.lane & 31;
 
   const int grp = p.num_q_heads / p.num_kv_heads;
+  // Heads qh .. qh + nh - 1 (one KV head: nh divides grp).
+  ker.nh = dq_ds_heads<D>(p);
+  const int hslots = p.num_q_heads / ker.nh;
   int qt, s, qh;
   if (tiles != nullptr) {
     int local, nt;
-    tiles->find(L / p.num_q_heads, s, local, nt);
+    tiles->find(L / hslots, s, local, nt);
     qt = nt - 1 - local;
-    qh = L % p.num_q_heads;
+    qh = L % hslots * ker.nh;
   } else {
-    const int per_qt = a.num_seqs * p.num_q_heads;
+    const int per_qt = a.num_seqs * hslots;
     qt = a.ntiles - 1 - L / per_qt;
     const int rem = L % per_qt;
-    s = rem / p.num_q_heads;
-    qh = rem % p.num_q_heads;
+    s = rem / hslots;
+    qh = rem % hslots * ker.nh;
   }
   const int kvh = qh / grp;
   ker.sq = resolve_seq(p, s);
@@ -1696,10 +1725,11 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
   int kt_hi[4];
   if constexpr (kBand) {
     if (dq_row_key_ends<C::kNW>(a, sq, i0, off, tid, (int*)smem_raw, kt_hi)) {
-      // A row reaches past the stored band: left to the recompute launch.
+      // A row reaches past the stored band: left to the recompute launch
+      // (one entry per query head).
       if (tid == 0 && a.dq_list != nullptr) {
-        const unsigned e = atomicAdd(&a.sched[3], 1u);
-        a.dq_list[e] = int2{s, (qt << 8) | qh};
+        const unsigned e = atomicAdd(&a.sched[3], (unsigned)ker.nh);
+        for (int h = 0; h < ker.nh; ++h) a.dq_list[e + h] = int2{s, (qt << 8) | (qh + h)};
       }
       return;
     }
@@ -1728,6 +1758,7 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
   ker.kstride = a.kl.token_stride;
   const int64_t row0 =
       (sq.packed ? sq.qtok / 32 + s : (int64_t)s * ((p.seqlen_q + 31) / 32)) + i0 / 32;
+  ker.ds_head_stride = (int64_t)a.ds_rows * a.ds_cols * 4096;
   if constexpr (kBand) {
     ker.ds_col_stride = 4096;
     ker.ds_copy_row = (const char*)a.ds + (((int64_t)qh * a.ds_rows + row0 + gc) * a.ds_cols) * 4096;
@@ -1739,9 +1770,11 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
   ker.trs.init(ker.lane);
   ker.kcp.init(ker.kstride, ker.wave, ker.lane);
 #pragma unroll
-  for (int g = 0; g < 2; ++g)
+  for (int h = 0; h < C::kHeads; ++h)
 #pragma unroll
-    for (int b = 0; b < C::kNBw; ++b) ker.acc[g][b] = f32x16{};
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int b = 0; b < C::kNBw; ++b) ker.acc[h][g][b] = f32x16{};
 
   const int g0 = 2 * ker.qpair;
   if (kt_begin < nkt) ker.issue(kt_begin, 0);
@@ -1751,7 +1784,7 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
     barrier_lds();  // tile kt landed; every wave is done with buffer cur ^ 1
     if (kt + 1 < nkt) ker.issue(kt + 1, cur ^ 1);
     const char G4_LDS* ktile = ker.smem + C::kLdsK + cur * C::kKTile;
-    const char G4_LDS* ds0 = ker.smem + C::kLdsDs + (cur * 4 + g0) * 4096;
+    const char G4_LDS* ds0 = ker.smem + C::kLdsDs + (cur * C::kHeads * 4 + g0) * 4096;
     const char G4_LDS* ds1 = ds0 + 4096;
     const bool v0 = kt >= ker.lo0 && kt <= ker.hi0, v1 = kt >= ker.lo1 && kt <= ker.hi1;
     // (The band kernel measured slower pipelined: 5.52 vs 5.39 ms on config 5;
@@ -1759,10 +1792,10 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
     if (!kBand && v0 && v1) {
       ker.ktile_both(ktile, ds0, ds1);
     } else {
-      ker.template kstep<0>(ktile, ds0, ds1, v0, v1);
-      ker.template kstep<1>(ktile, ds0, ds1, v0, v1);
-      ker.template kstep<2>(ktile, ds0, ds1, v0, v1);
-      ker.template kstep<3>(ktile, ds0, ds1, v0, v1);
+      ker.template kstep<0>(ktile, ds0, v0, v1);
+      ker.template kstep<1>(ktile, ds0, v0, v1);
+      ker.template kstep<2>(ktile, ds0, v0, v1);
+      ker.template kstep<3>(ktile, ds0, v0, v1);
     }
   }
 
@@ -1773,36 +1806,41 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
   // 32-row staging writes and the row reads free of bank conflicts) and
   // written back as whole rows.  Band tiles keep queries in accumulator
   // order, dense tiles in query order.
-  barrier_lds();  // every wave is done with the last key tile's operands
   char G4_LDS* stage = ker.smem;
   static_assert(C::kBM * C::kCPR * 16 <= C::kLdsBytes, "dQ staging tile");
-#pragma unroll
-  for (int g2 = 0; g2 < 2; ++g2) {
-    const int r = 32 * (g0 + g2) + (kBand ? ds_query_at(l32) : l32);
-#pragma unroll
-    for (int b = 0; b < C::kNBw; ++b)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int d = ker.dquart * C::kDW + b * 32 + 8 * r4 + 4 * ker.h32;
-        const f32x16& x = ker.acc[g2][b];
-        *(bf16x4 G4_LDS*)(stage + (r * C::kCPR + ((d >> 3) ^ (r & (C::kCPR - 1)))) * 16 +
-                          (d & 4) * 2) =
-            bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1], (__bf16)x[r4 * 4 + 2],
-                   (__bf16)x[r4 * 4 + 3]};
-      }
-  }
-  barrier_lds();
   constexpr int kRowsPerInst = 64 / C::kCPR;
 #pragma unroll
-  for (int j = 0; j < C::kBM / (C::kNW * kRowsPerInst); ++j) {
-    const int r = (j * C::kNW + ker.wave) * kRowsPerInst + ker.lane / C::kCPR;
-    const int c = ker.lane % C::kCPR;
-    const int my_i = i0 + r;
-    if (my_i < sq.lq) {
-      const bf16x8 v =
-          *(const bf16x8 G4_LDS*)(stage + (r * C::kCPR + (c ^ (r & (C::kCPR - 1)))) * 16);
-      __bf16* row = a.dq + tok_off(sq, s, sq.qtok, my_i, a.dql) + (int64_t)qh * a.dql.head_stride;
-      *(bf16x8*)(row + c * 8) = v;
+  for (int h = 0; h < C::kHeads; ++h) {
+    if (h >= ker.nh) break;
+    barrier_lds();  // every wave is done with the operands / the previous head's rows
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      const int r = 32 * (g0 + g2) + (kBand ? ds_query_at(l32) : l32);
+#pragma unroll
+      for (int b = 0; b < C::kNBw; ++b)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int d = ker.dquart * C::kDW + b * 32 + 8 * r4 + 4 * ker.h32;
+          const f32x16& x = ker.acc[h][g2][b];
+          *(bf16x4 G4_LDS*)(stage + (r * C::kCPR + ((d >> 3) ^ (r & (C::kCPR - 1)))) * 16 +
+                            (d & 4) * 2) =
+              bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1], (__bf16)x[r4 * 4 + 2],
+                     (__bf16)x[r4 * 4 + 3]};
+        }
+    }
+    barrier_lds();
+#pragma unroll
+    for (int j = 0; j < C::kBM / (C::kNW * kRowsPerInst); ++j) {
+      const int r = (j * C::kNW + ker.wave) * kRowsPerInst + ker.lane / C::kCPR;
+      const int c = ker.lane % C::kCPR;
+      const int my_i = i0 + r;
+      if (my_i < sq.lq) {
+        const bf16x8 v =
+            *(const bf16x8 G4_LDS*)(stage + (r * C::kCPR + (c ^ (r & (C::kCPR - 1)))) * 16);
+        __bf16* row =
+            a.dq + tok_off(sq, s, sq.qtok, my_i, a.dql) + (int64_t)(qh + h) * a.dql.head_stride;
+        *(bf16x8*)(row + c * 8) = v;
+      }
     }
   }
 }
@@ -1817,8 +1855,9 @@ __global__ void __launch_bounds__(DqDsCfg<D>::kNT, 1) dq_ds_kernel(BwdParams a) 
     SeqTiles tiles;
     tiles.init(a.p.cu_seqlens_q, a.num_seqs, DqDsCfg<D>::kBM);
     const bool compact = D == 256 && tiles.ok;
-    const unsigned n = compact ? (unsigned)(tiles.total * a.p.num_q_heads)
-                               : (unsigned)(a.num_seqs * a.ntiles * a.p.num_q_heads);
+    const int hslots = a.p.num_q_heads / dq_ds_heads<D>(a.p);
+    const unsigned n = compact ? (unsigned)(tiles.total * hslots)
+                               : (unsigned)(a.num_seqs * a.ntiles * hslots);
     PrefetchQueue q{a.sched + 2, n};
     for (int t = q.first(); q.valid(t); t = q.next((int G4_LDS*)smem_raw)) {
       q.draw();
@@ -1838,7 +1877,8 @@ static hipError_t launch_dq_ds(const BwdParams& a, hipStream_t stream) {
   static LdsAttr attr[2];
   BwdParams b = a;
   b.ntiles = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
-  const int64_t items = (int64_t)b.num_seqs * b.ntiles * a.p.num_q_heads;
+  const int64_t items =
+      (int64_t)b.num_seqs * b.ntiles * (a.p.num_q_heads / dq_ds_heads<D>(a.p));
   if (items <= 0) return hipSuccess;
   static PersistentGrid grid;
   bool queue = false;
