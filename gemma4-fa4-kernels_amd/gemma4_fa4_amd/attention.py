@@ -587,7 +587,10 @@ class _Plan:
             prob = self.problem()
             out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
             lse = torch.empty(self.lse_shape(), dtype=torch.float32, device=q.device)
-            ws = self._workspace(0, q.device, prob)
+            # Most forwards need no workspace (no vision IDs at head dim 256): the
+            # library takes NULL for a zero-byte workspace, so none is allocated.
+            ws_bytes = self.workspace_bytes(0, prob)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
         except Exception:
             self._settle()  # an invalid cu_seqlens is reported first
             raise
@@ -599,7 +602,7 @@ class _Plan:
                 k.data_ptr(), _layout(k, self.packed),
                 v.data_ptr(), _layout(v, self.packed),
                 out.data_ptr(), _layout(out, self.packed),
-                lse.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+                lse.data_ptr(), None if ws is None else ws.data_ptr(), ws_bytes, stream,
             )
             self._settle()
             rc = lib.g4_attn_fwd(*args)
