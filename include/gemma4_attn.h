@@ -89,7 +89,8 @@ int g4_abi_version(void);
 const char* g4_last_error(void);
 
 /* Bytes of workspace g4_attn_fwd (phase 0) or g4_attn_bwd (phase 1) needs.
- * Returns 0 and sets the error on an invalid problem. */
+ * Returns 0 and sets the error on an invalid problem.  A valid problem that
+ * needs no workspace (0 bytes) may pass a NULL workspace. */
 size_t g4_workspace_bytes(const g4_problem* p, int phase);
 
 /*
