@@ -112,9 +112,9 @@ __bf16* ds_ptr(const g4_problem& p, void* ws) {
 unsigned* sched_ptr(const g4_problem& p, void* ws) {
   return (unsigned*)((char*)ws + fwd_ws_bytes(p) + g4::delta_bytes(p) + g4::ds_bytes(p));
 }
-int2* dq_list_ptr(const g4_problem& p, void* ws) {
+int4* dq_list_ptr(const g4_problem& p, void* ws) {
   if (!g4::dq_list_bytes(p)) return nullptr;
-  return (int2*)((char*)sched_ptr(p, ws) + g4::kSchedBytes);
+  return (int4*)((char*)sched_ptr(p, ws) + g4::kSchedBytes);
 }
 
 // Forward workspace of g4_attn_fwd_static: a file-scope device array, one
@@ -244,12 +244,12 @@ size_t ds_bytes(const g4_problem& p) {
   const size_t b = (size_t)rows * cols * p.num_q_heads * 4096;
   return b <= ds_cap(p) ? b : 0;
 }
-// Head dim 256 stored-dS dQ with vision IDs: one 8-byte entry per possible
+// Head dim 256 stored-dS dQ with vision IDs: one 16-byte entry per possible
 // (sequence, 128-query tile, query head) for the tiles left to recompute.
 size_t dq_list_bytes(const g4_problem& p) {
   if (p.head_dim != 256 || !ds_bytes(p) || p.vision_ids == nullptr || !p.bidirectional_vision)
     return 0;
-  return align256((size_t)p.num_seqs * ((p.seqlen_q + 127) / 128) * p.num_q_heads * 8);
+  return align256((size_t)p.num_seqs * ((p.seqlen_q + 127) / 128) * p.num_q_heads * 16);
 }
 // Head dim 256 with vision and document IDs: a counter and one int per
 // (sequence, 128-query tile, query head) for the forward's second pass.

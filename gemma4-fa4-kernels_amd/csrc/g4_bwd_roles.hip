@@ -24,8 +24,8 @@
 // matrix core, so one's VALU and LDS work overlaps the other's MFMAs.
 //
 // A step is 32 query rows of one query head (steps walk the query tiles from
-// the last one down, the GQA group's heads innermost) with three workgroup
-// barriers:
+// the last one down, or up for the second key tile of a pair, the GQA group's
+// heads innermost) with three workgroup barriers:
 //   B1  the step's Q, dO, LSE / delta (and metadata) copies have landed in
 //       every wave.  P waves: copy the next Q tile (and row data) into the
 //       other buffer, partial S over their head-dim half, then write the eight
@@ -124,6 +124,7 @@ struct RolesKernel {
   bool has_vid, has_doc, has_meta;
   int my_vid, my_doc;
   int grp, kvh, qt_lo, nqt;
+  bool up;  // query tiles walked upward (else from the last one down)
   int64_t tq;
   int64_t ds_row0;  // dS tile row of this sequence's first query tile
   uint32_t ds_lane;  // byte offset of this lane's dS run inside a tile
@@ -137,7 +138,7 @@ struct RolesKernel {
   __device__ __forceinline__ void coords(int it, int& qh, int& i0) const {
     const int sh = __builtin_ctz(grp);  // grp is 1, 2, 4 or 8
     qh = kvh * grp + (it & (grp - 1));
-    i0 = (qt_lo + nqt - 1 - (it >> sh)) * C::kBM;
+    i0 = (up ? qt_lo + (it >> sh) : qt_lo + nqt - 1 - (it >> sh)) * C::kBM;
   }
 
   // One copy path for full and tail tiles (32-bit buffer offsets, rows
@@ -380,10 +381,11 @@ struct RolesKernel {
   }
 };
 
-// One key tile kt of sequence s and KV head kvh.
+// One key tile kt of sequence s and KV head kvh; its query tiles are walked
+// upward with `up`, else from the last one down.
 template <bool META, bool QUEUE>
 __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_raw, int kvh,
-                                                int s, int kt) {
+                                                int s, int kt, bool up) {
   // Rotation only in the one-item-per-workgroup launch: measured on config 2
   // (one 8192-token sequence) dK/dV 5.32 -> 5.17 ms, but 5.21 -> 5.89 ms in the
   // work-queue launch of config 4 (packed, 1-2048-token segments).
@@ -404,6 +406,7 @@ __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_r
 
   ker.grp = p.num_q_heads / p.num_kv_heads;
   ker.kvh = kvh;
+  ker.up = up;
   ker.s = s;
   ker.sq = resolve_seq(p, ker.s);
   const Seq& sq = ker.sq;
@@ -480,7 +483,14 @@ __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_r
 // longest sequences) first within a KV head.  Under the causal mask a key
 // tile's query count falls linearly with its index, so a pair carries about
 // the same number of steps whatever r is.  KV head slowest keeps the
-// workgroups of one XCD on one head group's Q and dO.
+// workgroups of one XCD on one head group's Q and dO, and the step order
+// keeps them on the same query tiles at the same time: the first tile walks
+// its query tiles from the last one down, the second from its first one up.
+// On one causal sequence of Q query tiles (two per key tile), after t query
+// tiles of steps a workgroup in its first pass is at query tile Q - 1 - t and
+// one in its second pass at t - 2, whatever its r, so the workgroups of an XCD
+// read two streams of Q and dO tiles between them (was: one per workgroup
+// once they restarted at the last tile at different times).
 // With `by_length` (the queue launch of a packed batch of up to 64
 // sequences): only the pairs that exist, sequence by sequence from the longest
 // (a pair's cost grows with its sequence's length, and a longer sequence has
@@ -514,7 +524,7 @@ __device__ __forceinline__ void dkdv_roles_pair(const BwdParams& a, char* smem_r
       if (kt == r) break;
       barrier_lds();  // every wave is done with the first tile's LDS
     }
-    dkdv_roles_tile<META, QUEUE>(a, smem_raw, kvh, s, kt);
+    dkdv_roles_tile<META, QUEUE>(a, smem_raw, kvh, s, kt, pass == 1);
   }
 }
 
@@ -1339,10 +1349,10 @@ __device__ __forceinline__ void dq_roles256_item(const BwdParams& a, char* smem_
   const bool listed = a.dq_recompute_only && a.dq_list != nullptr;
   if (listed) {
     // Entry L of the stored-dS pass's list: a tile known to need recomputing.
-    const int2 e = a.dq_list[L];
+    const int4 e = a.dq_list[L];
     s = __builtin_amdgcn_readfirstlane(e.x);
-    qt = __builtin_amdgcn_readfirstlane(e.y) >> 8;
-    qh = __builtin_amdgcn_readfirstlane(e.y) & 255;
+    qt = __builtin_amdgcn_readfirstlane(e.y);
+    qh = __builtin_amdgcn_readfirstlane(e.z);
     kvh = qh / grp;
   } else {
     const int per_kvh = a.num_seqs * a.ntiles * grp;
@@ -1729,7 +1739,7 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
       // (one entry per query head).
       if (tid == 0 && a.dq_list != nullptr) {
         const unsigned e = atomicAdd(&a.sched[3], (unsigned)ker.nh);
-        for (int h = 0; h < ker.nh; ++h) a.dq_list[e + h] = int2{s, (qt << 8) | (qh + h)};
+        for (int h = 0; h < ker.nh; ++h) a.dq_list[e + h] = int4{s, qt, qh + h, 0};
       }
       return;
     }

@@ -82,9 +82,9 @@ struct BwdParams {
   // counts the entries of dq_list.
   unsigned* sched;
   // Head dim 256 with vision IDs: the query tiles the stored-dS dQ pass left
-  // for recomputation, appended by that pass ({sequence, query tile << 8 |
-  // query head}; order not significant: each entry writes its own dQ rows).
-  int2* dq_list;
+  // for recomputation, appended by that pass ({sequence, query tile, query
+  // head, 0}; order not significant: each entry writes its own dQ rows).
+  int4* dq_list;
 };
 
 // Workspace layout helpers (bytes).

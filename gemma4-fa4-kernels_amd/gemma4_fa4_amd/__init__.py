@@ -14,6 +14,7 @@ from .attention import (
     fa4_local_forward,
     fa4_local_text_forward,
     fa4_local_varlen_forward,
+    pin_backward_ds_budget,
 )
 from . import torch_ops
 from .errors import GlobalBackwardBudgetExceeded, UnsupportedH100Path, UnsupportedMI355XPath
@@ -63,6 +64,7 @@ __all__ = [
     "fa4_global_forward_only",
     "fa4_global_varlen_forward",
     "fa4_global_varlen_forward_only",
+    "pin_backward_ds_budget",
     "prepare_global_kv_from_projection_source",
     "GlobalBackwardBudgetExceeded",
     "UnsupportedH100Path",

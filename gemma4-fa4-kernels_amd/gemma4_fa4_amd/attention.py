@@ -528,8 +528,12 @@ class _Plan:
     vision: torch.Tensor | None = None
     documents: torch.Tensor | None = None
     # Bytes of the backward workspace for stored dS tiles (0: library default,
-    # negative: none, so the dQ stage recomputes S and dP).
+    # negative: none, so the dQ stage recomputes S and dP).  Fitted again to the
+    # free HBM at backward time (_refit_backward).
     ds_budget: int = 0
+    # Global layers fail closed at backward time when even the recompute route
+    # does not fit the guarded budget (GlobalBackwardBudgetExceeded).
+    global_backward: bool = False
     # Cumulative-array checks still to run before the first launch.
     pending: _CumulativeCheck | None = field(default=None, repr=False, compare=False)
 
@@ -611,6 +615,7 @@ class _Plan:
 
     def backward(self, q, k, v, out, dout, lse, dlse):
         lib = _lib.load()
+        _refit_backward(self, q, k, v)  # before anything is allocated
         if not _meets_operand_contract(dout):
             # e.g. a broadcast gradient of a sum, or a view off 16-byte alignment
             dout = dout.contiguous()
@@ -765,16 +770,66 @@ def _fit_ds_budget(plan: _Plan, q, k, v, budget: int) -> int:
     return lean
 
 
+# Stored-dS budget pinned by the caller (None: fitted to the free HBM).
+_PINNED_DS_BUDGET: int | None = None
+
+
+def pin_backward_ds_budget(nbytes: int | None) -> int | None:
+    """Pin the backward's stored-dS budget for every later call; returns the previous pin.
+
+    ``None`` (the default) fits the budget to the free HBM at each forward and
+    again at each backward: the dK/dV stage stores dS tiles while they fit, else
+    the dQ stage recomputes S and dP.  The two routes sum dQ in different
+    orders, so with the default the bits of dQ can depend on how much HBM is
+    free.  A pinned budget fixes the route: a negative value always
+    recomputes, a positive one stores the tiles that fit in that many bytes, 0
+    is the library's default cap (16 GiB).  The global layers still raise
+    ``GlobalBackwardBudgetExceeded`` when the pinned route does not fit the
+    guarded budget.  A process-wide setting (not per thread).
+    """
+    global _PINNED_DS_BUDGET
+    if nbytes is not None and not isinstance(nbytes, int):
+        raise TypeError("nbytes must be an int or None")
+    previous, _PINNED_DS_BUDGET = _PINNED_DS_BUDGET, nbytes
+    return previous
+
+
+def _fit_or_pin(plan: _Plan, q, k, v, free: int) -> int:
+    if _PINNED_DS_BUDGET is not None:
+        plan.ds_budget = _PINNED_DS_BUDGET
+        return _backward_additional_bytes(plan, q, k, v)
+    return _fit_ds_budget(plan, q, k, v, _global_backward_budget(free))
+
+
 def _preflight_backward(plan: _Plan, q, k, v) -> None:
+    plan.global_backward = True
     free = _free_hbm(q.device)
-    required = _fit_ds_budget(plan, q, k, v, _global_backward_budget(free))
+    required = _fit_or_pin(plan, q, k, v, free)
     _check_global_backward_budget(required, free)
 
 
 def _fit_local_backward(plan: _Plan, q, k, v) -> None:
     # The local backward has no budget error in the reference (FA4's autograd
     # allocates what it needs); its stored-dS band just shrinks to what fits.
-    _fit_ds_budget(plan, q, k, v, _global_backward_budget(_free_hbm(q.device)))
+    _fit_or_pin(plan, q, k, v, _free_hbm(q.device))
+
+
+def _refit_backward(plan: _Plan, q, k, v) -> None:
+    """Fit the dS budget again to the HBM free when the backward starts.
+
+    The reference measures free HBM inside the global backward, before it
+    allocates its scratch, and fails closed there
+    (patches/flash-attention/0002-sm90-gemma4-d512-forward-backward.patch:1164-1181).
+    Between a layer's forward and its backward a training step allocates the
+    other layers' activations, so the forward's fit can be stale: the route
+    (stored dS or recompute) is chosen again here, and a global layer whose
+    lean route no longer fits raises GlobalBackwardBudgetExceeded instead of
+    running out of memory in the allocation.
+    """
+    free = _free_hbm(q.device)
+    required = _fit_or_pin(plan, q, k, v, free)
+    if plan.global_backward:
+        _check_global_backward_budget(required, free)
 
 
 def _preflight_forward_outputs(q: torch.Tensor) -> None:

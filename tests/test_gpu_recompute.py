@@ -138,12 +138,38 @@ def test_d256_budget_between_the_band_and_its_vision_extension():
     full = plan.workspace_bytes(1)
     plan.ds_budget = -1
     # only the band is stored, plus the list of query tiles the stored-dS dQ
-    # pass leaves for recomputation (8 bytes per 128-query tile and head)
-    listed = -(-(((2600 + 127) // 128) * 32 * 8) // 256) * 256
+    # pass leaves for recomputation (16 bytes per 128-query tile and head)
+    listed = -(-(((2600 + 127) // 128) * 32 * 16) // 256) * 256
     assert full - plan.workspace_bytes(1) == band + listed
     (o_ref, l_ref, *refs), bf = _oracle(q, k, v, do, dlse, cq, ck, 1024, vis)
     check_forward(got[0], got[1], o_ref, l_ref, local=True, label="partial band")
     check_gradients(got[2:], refs, bf, label="partial band")
+
+
+def test_d256_listed_recompute_past_255_query_heads():
+    # The recompute list keeps the query head in a field of its own, so heads
+    # past 255 are recomputed as themselves (an 8-bit head field would wrap
+    # 256.. onto 0..).  288 query heads, GQA 2, the partial-band budget of the
+    # test above; checked on heads either side of 256.
+    lq = lk = [2600]
+    hq, hkv = 288, 144
+    q, k, v, do, dlse = qkv(9400, 2600, 2600, hq, hkv, 256)
+    cq, ck = cu(lq), cu(lk)
+    vis = torch.full((2600,), -1, dtype=torch.int32)
+    vis[400:1500] = 0
+    vis[1800:2100] = 1
+    band = (2600 // 32 + 1) * 18 * hq * 4096
+    got, plan = _stages(q, k, v, do, dlse, cq, ck, 1024, vis=vis, ds_budget=band + 4096)
+    heads = [0, 1, 254, 255, 256, 257, 286, 287]
+    kvs = sorted({h // 2 for h in heads})
+    (o_ref, l_ref, dq_ref, dk_ref, dv_ref), (bq, bk, bv) = _oracle(
+        q, k, v, do, dlse, cq, ck, 1024, vis, heads=heads)
+    label = "288 query heads, listed recompute"
+    check_forward(got[0][:, heads], got[1][heads], o_ref[:, heads], l_ref[heads], local=True,
+                  label=label)
+    check_gradients([got[2][:, heads], got[3][:, kvs], got[4][:, kvs]],
+                    [dq_ref[:, heads], dk_ref[:, kvs], dv_ref[:, kvs]],
+                    [bq[:, heads], bk[:, kvs], bv[:, kvs]], label=label)
 
 
 def test_global_sequence_past_the_default_ds_budget():

@@ -365,6 +365,95 @@ def test_backward_budget_drops_stored_ds_before_failing(monkeypatch):
         att._preflight_backward(plan, q, k, v)
 
 
+def _global_plan_s4096():
+    s = 4096
+    q = torch.empty(s, 32, 512, dtype=torch.bfloat16)
+    k = torch.empty(s, 4, 512, dtype=torch.bfloat16)
+    v = torch.empty(s, 4, 512, dtype=torch.bfloat16)
+    cu = torch.tensor([0, s], dtype=torch.int32)
+    return att._packed_plan(q, k, cu, cu, s, s, g.GLOBAL_ATTENTION), q, k, v
+
+
+def _free_for(budget):  # free bytes whose guarded budget is `budget`
+    return max(budget * 5 // 4 + 4, budget + 2 * 1024 ** 3)
+
+
+def test_backward_refits_the_ds_budget_when_free_hbm_shrinks(monkeypatch):
+    # The forward fits the stored-dS route to the HBM free then; by the
+    # backward other allocations may have taken it.  The backward fits again
+    # before allocating (patch 0002:1164-1181 measures free HBM there): the
+    # recompute route when the tiles no longer fit, the typed error when even
+    # that does not.
+    plan, q, k, v = _global_plan_s4096()
+    plan.ds_budget = 0
+    full = att._backward_additional_bytes(plan, q, k, v)
+    plan.ds_budget = -1
+    lean = att._backward_additional_bytes(plan, q, k, v)
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: _free_for(full))
+    att._preflight_backward(plan, q, k, v)  # forward time: everything fits
+    assert plan.ds_budget == 0 and plan.global_backward
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: _free_for(lean))
+    att._refit_backward(plan, q, k, v)  # backward time: only the lean route fits
+    assert att._backward_additional_bytes(plan, q, k, v) == lean
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: _free_for(full))
+    att._refit_backward(plan, q, k, v)  # memory came back: tiles stored again
+    assert plan.ds_budget == 0
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: _free_for(lean - 1))
+    with pytest.raises(g.GlobalBackwardBudgetExceeded):
+        att._refit_backward(plan, q, k, v)
+    # a local layer shrinks its band instead of failing
+    local = att._packed_plan(q[:, :, :256], k[:, :, :256].repeat(1, 4, 1), plan.cu_q, plan.cu_k,
+                             4096, 4096, g.SLIDING_ATTENTION)
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: 1)
+    att._refit_backward(local, q[:, :, :256], k[:, :, :256].repeat(1, 4, 1),
+                        v[:, :, :256].repeat(1, 4, 1))
+    assert local.ds_budget < 0 and not local.global_backward
+
+
+def test_backward_fits_before_it_allocates(monkeypatch):
+    plan, q, k, v = _global_plan_s4096()
+
+    class Refit(Exception):
+        pass
+
+    def refit(*_a):
+        raise Refit
+
+    monkeypatch.setattr(att, "_refit_backward", refit)
+    allocated = []
+    monkeypatch.setattr(plan, "_workspace", lambda *a, **kw: allocated.append(a))
+    with pytest.raises(Refit):
+        plan.backward(q, k, v, q, q, torch.empty(32, 4096), None)
+    assert not allocated
+
+
+def test_pinned_ds_budget_fixes_the_route(monkeypatch):
+    # With the budget pinned the route no longer depends on the free HBM (the
+    # two routes sum dQ in different orders); the global layer still fails
+    # closed when the pinned route does not fit.
+    plan, q, k, v = _global_plan_s4096()
+    plan.ds_budget = -1
+    lean = att._backward_additional_bytes(plan, q, k, v)
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: 1 << 50)
+    previous = g.pin_backward_ds_budget(-1)
+    try:
+        assert previous is None
+        att._preflight_backward(plan, q, k, v)
+        assert plan.ds_budget == -1
+        att._refit_backward(plan, q, k, v)
+        assert plan.ds_budget == -1
+        monkeypatch.setattr(att, "_free_hbm", lambda _d: _free_for(lean - 1))
+        with pytest.raises(g.GlobalBackwardBudgetExceeded):
+            att._refit_backward(plan, q, k, v)
+        with pytest.raises(TypeError):
+            g.pin_backward_ds_budget(1.5)
+    finally:
+        assert g.pin_backward_ds_budget(previous) == -1
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: 1 << 50)
+    att._refit_backward(plan, q, k, v)
+    assert plan.ds_budget == 0
+
+
 def test_row_preparation_validation_happens_before_any_launch():
     # Host-side checks of g4_kv_prep_fwd / _bwd with fake addresses: nothing
     # reaches the device when a check fails.
