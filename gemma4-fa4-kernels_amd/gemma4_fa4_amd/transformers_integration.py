@@ -42,6 +42,13 @@ fit.
 Padded query rows (2D padding mask) are returned as zeros with LSE ``-inf``,
 as the reference's unpacking does (ti.py:1418-1447).
 
+An eager ``StaticCache`` hands over its whole physical K/V backing, whose tail
+past the written positions is unwritten.  With the reference's contract (B=1,
+no gradient, text only, no documents, no explicit packed lengths, K offset 0,
+a contiguous valid K prefix) the call is trimmed to the active prefix
+``q_offset + Sq - kv_offset`` before routing (ti.py:1020-1110, 1815-1845); a
+mask callable that is not the native plan must also mask every trimmed key.
+
 Under ``torch.compile`` or with FakeTensor inputs, a text-only single
 sequence (B = 1, S <= 1024, the layer's causal / sliding-causal mask, explicit
 position_ids) is routed to one opaque custom operator of ``torch_ops``
@@ -55,7 +62,7 @@ instead.
 from __future__ import annotations
 
 import types
-from dataclasses import dataclass
+from dataclasses import dataclass, replace
 from typing import Any, Callable
 
 import torch
@@ -369,6 +376,82 @@ def _lower_right(plan: Gemma4MaskPlan) -> bool:
     except TypeError:
         return False
     return q_off - kv_off == plan.kv_length - plan.q_length
+
+
+def _static_cache_prefix(query, key, value, plan: Gemma4MaskPlan, *, trusted: bool,
+                         vision, documents, grad: bool, explicit_packed: bool):
+    """Trim an underfilled eager StaticCache to its active K prefix (ti.py:1020-1110).
+
+    A StaticCache layer returns its whole physical K/V backing after the
+    update, while the mask plan was built before it: the query offset and
+    the K offset give the active length ``q_offset + Sq - kv_offset``.
+    Returns ``(key, value, plan, vision, trimmed)``; raises
+    ``UnsupportedMI355XPath`` with the reference's messages where its B1
+    text-only no-grad contract does not hold.  Nothing is copied: K and V are
+    views of the physical backing.
+    """
+    physical_k = key.shape[2]
+    try:
+        q_offset = _as_int(plan.q_offset, name="q_offset")
+        kv_offset = _as_int(plan.kv_offset, name="kv_offset")
+    except TypeError as exc:
+        raise UnsupportedMI355XPath(
+            "eager StaticCache active-prefix offsets must be real scalar integers"
+        ) from exc
+    logical_k = q_offset + query.shape[2] - kv_offset
+    if logical_k == physical_k:
+        return key, value, plan, vision, False
+    if logical_k <= 0 or logical_k > physical_k:
+        raise UnsupportedMI355XPath(
+            "eager StaticCache active K length is outside the physical K/V backing"
+        )
+    if q_offset < 0 or kv_offset < 0 or q_offset < kv_offset:
+        raise UnsupportedMI355XPath(
+            "eager StaticCache offsets must describe a nonnegative lower-right prefix"
+        )
+    if kv_offset != 0:
+        raise UnsupportedMI355XPath(
+            "an underfilled eager StaticCache prefix must start at physical K offset zero"
+        )
+    if query.shape[0] != 1:
+        raise UnsupportedMI355XPath("eager StaticCache normalization accepts B1 only")
+    if grad:
+        raise UnsupportedMI355XPath("eager StaticCache normalization is inference-only")
+    if explicit_packed:
+        raise UnsupportedMI355XPath(
+            "eager StaticCache normalization does not accept explicit packed lengths"
+        )
+    if documents is not None:
+        raise UnsupportedMI355XPath(
+            "eager StaticCache normalization does not accept document metadata"
+        )
+    if vision is not None:
+        if bool((vision >= 0).any().item()):
+            raise UnsupportedMI355XPath(
+                "eager StaticCache normalization accepts text-only vision metadata"
+            )
+        vision = None
+    padding = _padding(plan, query.device)
+    if padding is not None and (
+        padding.shape != (1, physical_k) or not bool(padding[0, :logical_k].all().item())
+    ):
+        raise UnsupportedMI355XPath("eager StaticCache requires one contiguous valid K prefix")
+    if not trusted:
+        # The native plan masks every trimmed key (each lies past the last
+        # query); another callable must be shown to do so on all of them.
+        dev = query.device
+        q_pos = torch.arange(q_offset, q_offset + query.shape[2], device=dev)
+        tail = torch.arange(kv_offset + logical_k, kv_offset + physical_k, device=dev)
+        if bool(_eval_mask_rows(plan.mask_function, 0, q_pos, tail).any().item()):
+            raise UnsupportedMI355XPath(
+                "the mask admits keys past the eager StaticCache active prefix"
+            )
+    mask = plan.attention_mask
+    trimmed = replace(plan, kv_length=logical_k,
+                      attention_mask=None if mask is None else mask[:, :logical_k])
+    if getattr(plan, "_g4_origin", None) is _NATIVE_ORIGIN:
+        object.__setattr__(trimmed, "_g4_origin", _NATIVE_ORIGIN)
+    return key[:, :, :logical_k, :], value[:, :, :logical_k, :], trimmed, vision, True
 
 
 def _run_starts(*rows: torch.Tensor) -> torch.Tensor:
@@ -839,9 +922,21 @@ def gemma4_fa4_prepared(
         position_ids = position_ids.to(torch.int64).expand(B, -1)
     vision = _rows(vision_block_ids, name="vision_block_ids", batch=B, length=Sk, device=device, pad=-1)
     documents = _rows(document_ids, name="document_ids", batch=B, length=Sk, device=device, pad=-1)
-    padding = _padding(plan, device)
 
     trusted = plan.mask_function is None or getattr(plan, "_g4_origin", None) is _NATIVE_ORIGIN
+    grad = torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value))
+    key, value, plan, vision, trimmed = _static_cache_prefix(
+        query, key, value, plan, trusted=trusted, vision=vision, documents=documents, grad=grad,
+        explicit_packed=any(x is not None for x in (cu_seq_lens_q, cu_seq_lens_k, max_length_q,
+                                                       max_length_k)),
+    )
+    if trimmed:
+        Sk = key.shape[2]
+        # A cache is present: position_ids restarts are not packing boundaries
+        # (ti.py:1831-1835).
+        position_ids = None
+    padding = _padding(plan, device)
+
     if trusted and not _lower_right(plan):
         raise UnsupportedMI355XPath("cache/query offsets are not the native lower-right alignment")
     structural = None
@@ -923,7 +1018,6 @@ def gemma4_fa4_prepared(
                 "(unrecognised callable, non-lower-right offsets, or missing vision metadata)"
             )
 
-    grad = torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value))
     single = B == 1 and Sq == Sk and segs.count == 1 and segs.all_valid and documents is None
 
     if not local:

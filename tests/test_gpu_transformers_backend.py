@@ -177,3 +177,37 @@ def test_evaluation_proof_rejects_a_different_callable():
     q, k, v = _bhsd(LOCAL_LAYER, 1, s, s, seed=16)
     with pytest.raises(UnsupportedMI355XPath, match="not provably"):
         ti.gemma4_fa4_prepared(_module(LOCAL_LAYER), q, k, v, plan, **_kw(LOCAL_LAYER))
+
+
+@pytest.mark.parametrize("layer,physical,active,sq", [
+    (LOCAL_LAYER, 2048, 1500, 1),
+    (LOCAL_LAYER, 2048, 1500, 4),
+    (GLOBAL_LAYER, 4096, 3000, 1),
+], ids=["local-decode", "local-chunk", "global-decode"])
+def test_static_cache_underfilled_prefix_routes_natively(layer, physical, active, sq):
+    # Eager StaticCache: the layer hands over its whole physical backing; keys
+    # past the active prefix were never written.  The call is trimmed to the
+    # prefix (reference ti.py:1020-1110) and runs on the kernels: the result
+    # matches dense attention over the prefix and does not depend on the tail.
+    print(f"static cache layer={layer} physical={physical} active={active} sq={sq}", flush=True)
+    q, k, v = _bhsd(layer, 1, sq, physical, seed=17)
+    fn = mu.sliding_window_causal_mask_function(1024) if layer == LOCAL_LAYER else mu.causal_mask_function
+    plan = ti.gemma4_fa4_mask(1, sq, physical, q_offset=active - sq, kv_offset=0,
+                              mask_function=fn,
+                              attention_mask=torch.ones((1, active), dtype=torch.long, device=DEV))
+    k[:, :, active:] = 3e4
+    v[:, :, active:] = -3e4
+    with torch.no_grad():
+        first = ti.gemma4_fa4_prepared(_module(layer), q, k, v, plan, **_kw(layer))
+        k[:, :, active:] = -1e4
+        v[:, :, active:] = 7e3
+        second = ti.gemma4_fa4_prepared(_module(layer), q, k, v, plan, **_kw(layer))
+    torch.cuda.synchronize()
+    assert first.path == ("fa4_local_varlen" if layer == LOCAL_LAYER else "fa4_global_forward_only")
+    assert torch.equal(first.output, second.output) and torch.equal(first.lse, second.lse)
+    qi = torch.arange(sq, device=DEV)[:, None] + active - sq
+    ki = torch.arange(active, device=DEV)[None, :]
+    allowed = ki <= qi
+    if layer == LOCAL_LAYER:
+        allowed &= ki > qi - 1024
+    _check(first, q, k[:, :, :active], v[:, :, :active], allowed[None], layer)

@@ -399,12 +399,190 @@ def test_lower_right_query_suffix_routes_varlen_with_the_kv_offset(native):
 
 
 def test_non_lower_right_offsets_fail_closed(native):
-    plan = ti.gemma4_fa4_mask(1, 6, 16, q_offset=4, kv_offset=0,
-                              mask_function=mu.sliding_window_causal_mask_function(1024))
+    # Queries past the physical K (no lower-right alignment, not a cache
+    # prefix), and an under-filled K with gradients (the StaticCache prefix
+    # normalisation is inference-only), both fail closed before any launch.
+    fn = mu.sliding_window_causal_mask_function(1024)
+    plan = ti.gemma4_fa4_mask(1, 6, 16, q_offset=12, kv_offset=0, mask_function=fn)
     q, k, v = _bhsd(LOCAL_LAYER, 1, 6, 16)
-    with pytest.raises(UnsupportedMI355XPath):
+    with pytest.raises(UnsupportedMI355XPath, match="outside the physical K/V backing"):
+        ti.gemma4_fa4_prepared(_module(LOCAL_LAYER), q, k, v, plan, **_kwargs(LOCAL_LAYER))
+    plan = ti.gemma4_fa4_mask(1, 6, 16, q_offset=4, kv_offset=0, mask_function=fn)
+    q, k, v = _bhsd(LOCAL_LAYER, 1, 6, 16, grad=True)
+    with pytest.raises(UnsupportedMI355XPath, match="inference-only"):
         ti.gemma4_fa4_prepared(_module(LOCAL_LAYER), q, k, v, plan, **_kwargs(LOCAL_LAYER))
     assert not native
+
+
+# ----------------------------------------------------------------------------
+# Eager StaticCache active prefix (reference tests/test_transformers_integration.py:1180-1465)
+# ----------------------------------------------------------------------------
+
+
+@pytest.fixture
+def received(native, monkeypatch):
+    """The Q/K/V tensors each (stand-in) adapter receives, in call order."""
+    seen = []
+    for name in ("fa4_local_forward", "fa4_global_text_forward", "fa4_global_forward_only",
+                 "fa4_local_varlen_forward", "fa4_global_varlen_forward",
+                 "fa4_global_varlen_forward_only"):
+        inner = getattr(ti, name)
+
+        def wrap(*args, _inner=inner, _name=name, **kwargs):
+            seen.append((_name, args[:3]))
+            return _inner(*args, **kwargs)
+
+        monkeypatch.setattr(ti, name, wrap)
+    return seen
+
+
+def _static_cache(layer, *, sq=2, physical=8, q_offset=3, style="short", callable_=False,
+                  seed=21):
+    # Under-filled StaticCache: queries at q_offset .. q_offset + sq - 1 over
+    # a physical backing whose keys past them were never written (filled here
+    # with hostile values that must not reach the kernels).
+    q, k, v = _bhsd(layer, 1, sq, physical, seed=seed)
+    active = q_offset + sq
+    k[:, :, active:] = 127
+    v[:, :, active:] = -91
+    mask = {
+        "short": torch.ones((1, active), dtype=torch.int32),
+        "physical-zero-tail": torch.tensor([[1] * active + [0] * (physical - active)],
+                                           dtype=torch.int32),
+        "physical-all-ones": torch.ones((1, physical), dtype=torch.int32),
+    }[style]
+    fn = None
+    if callable_:
+        fn = (mu.sliding_window_causal_mask_function(1024) if layer == LOCAL_LAYER
+              else mu.causal_mask_function)
+    plan = ti.gemma4_fa4_mask(1, sq, physical,
+                              q_offset=torch.tensor(q_offset) if layer == GLOBAL_LAYER else q_offset,
+                              kv_offset=0, mask_function=fn, attention_mask=mask)
+    return q, k, v, plan, active
+
+
+def _causal_allowed(sq, sk, q_offset, window=None):
+    qi = torch.arange(sq)[:, None] + q_offset
+    ki = torch.arange(sk)[None, :]
+    allowed = ki <= qi
+    if window:
+        allowed &= ki > qi - window
+    return allowed[None]
+
+
+@pytest.mark.parametrize("callable_", [False, True], ids=["native-plan", "hf-callable"])
+@pytest.mark.parametrize("style", ["short", "physical-zero-tail", "physical-all-ones"])
+@pytest.mark.parametrize("layer", [LOCAL_LAYER, GLOBAL_LAYER], ids=["local", "global"])
+def test_static_cache_underfilled_prefix_routes_trimmed_views(native, received, layer, style,
+                                                             callable_):
+    q, k, v, plan, active = _static_cache(layer, style=style, callable_=callable_)
+    res = ti.gemma4_fa4_prepared(_module(layer), q, k, v, plan, **_kwargs(layer))
+    name, (q_arg, k_arg, v_arg) = received[-1]
+    assert name == ("fa4_local_varlen_forward" if layer == LOCAL_LAYER
+                    else "fa4_global_varlen_forward_only")
+    # only the active prefix, as views of the cache's own storage
+    for phys, arg in ((k, k_arg), (v, v_arg)):
+        expected = phys[:, :, :active].transpose(1, 2)[0]
+        assert arg.shape == expected.shape and arg.stride() == expected.stride()
+        assert arg.storage_offset() == expected.storage_offset()
+        assert arg.untyped_storage().data_ptr() == phys.untyped_storage().data_ptr()
+    assert q_arg.untyped_storage().data_ptr() == q.untyped_storage().data_ptr()
+    assert native[-1][1:5] == ([0, 2], [0, active], 2, active)
+    window = 1024 if layer == LOCAL_LAYER else None
+    _check_against_dense(res, q, k[:, :, :active], v[:, :, :active],
+                         _causal_allowed(2, active, 3, window))
+    assert res.output.shape == (1, 2, q.shape[1], q.shape[-1]) and res.lse.shape == (1, q.shape[1], 2)
+
+
+@pytest.mark.parametrize("layer", [LOCAL_LAYER, GLOBAL_LAYER], ids=["local", "global"])
+def test_static_cache_hostile_unwritten_tail_is_absent(native, layer):
+    q, k, v, plan, active = _static_cache(layer)
+    first = ti.gemma4_fa4_prepared(_module(layer), q, k, v, plan, **_kwargs(layer))
+    k[:, :, active:] = -63
+    v[:, :, active:] = 119
+    second = ti.gemma4_fa4_prepared(_module(layer), q, k, v, plan, **_kwargs(layer))
+    assert torch.equal(first.output, second.output) and torch.equal(first.lse, second.lse)
+
+
+@pytest.mark.parametrize("layer", [LOCAL_LAYER, GLOBAL_LAYER], ids=["local", "global"])
+def test_static_cache_trim_does_not_read_position_resets_as_packing(native, layer):
+    # The trimmed call has Sq == Sk; with a cache present, position_ids
+    # restarts are not sequence boundaries (ti.py:1831-1835).
+    q, k, v = _bhsd(layer, 1, 5, 8, seed=22)
+    plan = ti.gemma4_fa4_mask(1, 5, 8, q_offset=0, kv_offset=0,
+                              attention_mask=torch.ones((1, 8), dtype=torch.int32))
+    pos = torch.tensor([[0, 1, 0, 1, 2]])
+    res = ti.gemma4_fa4_prepared(_module(layer), q, k, v, plan, position_ids=pos, **_kwargs(layer))
+    assert res.path == ("fa4_local_fixed" if layer == LOCAL_LAYER else "fa4_global_fixed")
+    window = 1024 if layer == LOCAL_LAYER else None
+    _check_against_dense(res, q, k[:, :, :5], v[:, :, :5], _causal_allowed(5, 5, 0, window))
+
+
+def test_static_cache_all_negative_vision_metadata_is_text_only(native):
+    q, k, v, plan, _active = _static_cache(LOCAL_LAYER)
+    res = ti.gemma4_fa4_prepared(_module(LOCAL_LAYER), q, k, v, plan,
+                                 vision_block_ids=torch.full((1, 8), -1, dtype=torch.int32),
+                                 **_kwargs(LOCAL_LAYER))
+    assert res.path == "fa4_local_varlen" and native[-1][5] is None
+
+
+@pytest.mark.parametrize(("extra", "grad", "batch", "error"), [
+    ({"vision_block_ids": torch.tensor([[0, -1, -1, -1, -1, -1, -1, -1]])}, False, 1,
+     "text-only vision metadata"),
+    ({"document_ids": torch.zeros((1, 8), dtype=torch.int32)}, False, 1, "document metadata"),
+    ({"cu_seq_lens_q": torch.tensor([0, 2], dtype=torch.int32),
+      "cu_seq_lens_k": torch.tensor([0, 5], dtype=torch.int32)}, False, 1,
+     "explicit packed lengths"),
+    ({}, True, 1, "inference-only"),
+    ({}, False, 2, "B1 only"),
+], ids=["active-vision", "documents", "explicit-cu", "grad", "batch2"])
+def test_static_cache_underfilled_prefix_outside_the_contract_fails_closed(native, extra, grad,
+                                                                          batch, error):
+    q, k, v = _bhsd(LOCAL_LAYER, batch, 2, 8, grad=grad)
+    plan = ti.gemma4_fa4_mask(batch, 2, 8, q_offset=3, kv_offset=0,
+                              attention_mask=torch.ones((batch, 8), dtype=torch.int32))
+    with pytest.raises(UnsupportedMI355XPath, match=error):
+        ti.gemma4_fa4_prepared(_module(LOCAL_LAYER), q, k, v, plan, **_kwargs(LOCAL_LAYER), **extra)
+    assert not native
+
+
+def test_static_cache_underfilled_prefix_rejects_nonzero_kv_offset(native):
+    q, k, v = _bhsd(LOCAL_LAYER, 1, 2, 8)
+    plan = ti.gemma4_fa4_mask(1, 2, 8, q_offset=4, kv_offset=1,
+                              attention_mask=torch.ones((1, 9), dtype=torch.int32))
+    with pytest.raises(UnsupportedMI355XPath, match="physical K offset zero"):
+        ti.gemma4_fa4_prepared(_module(LOCAL_LAYER), q, k, v, plan, **_kwargs(LOCAL_LAYER))
+    assert not native
+
+
+def test_static_cache_prefix_needs_a_contiguous_valid_prefix(native):
+    q, k, v = _bhsd(LOCAL_LAYER, 1, 2, 8)
+    plan = ti.gemma4_fa4_mask(1, 2, 8, q_offset=3, kv_offset=0,
+                              attention_mask=torch.tensor([[1, 1, 0, 1, 1, 0, 0, 0]]))
+    with pytest.raises(UnsupportedMI355XPath, match="contiguous valid K prefix"):
+        ti.gemma4_fa4_prepared(_module(LOCAL_LAYER), q, k, v, plan, **_kwargs(LOCAL_LAYER))
+    assert not native
+
+
+def test_static_cache_trim_needs_the_callable_to_mask_the_tail(native):
+    # A callable that is not the native predicate and admits a trimmed key
+    # (here: everything) must not be trimmed, whatever it does elsewhere.
+    q, k, v = _bhsd(LOCAL_LAYER, 1, 2, 8)
+    plan = ti.gemma4_fa4_mask(1, 2, 8, q_offset=3, kv_offset=0,
+                              mask_function=lambda b, h, qi, ki: torch.ones_like(qi * ki, dtype=torch.bool))
+    with pytest.raises(UnsupportedMI355XPath, match="past the eager StaticCache active prefix"):
+        ti.gemma4_fa4_prepared(_module(LOCAL_LAYER), q, k, v, plan, **_kwargs(LOCAL_LAYER))
+    assert not native
+
+
+def test_static_cache_rolled_local_window_keeps_the_full_physical_view(native):
+    # A full sliding cache (kv_offset 1 after one roll): the active length is
+    # the physical length, so nothing is trimmed.
+    q, k, v = _bhsd(LOCAL_LAYER, 1, 1, 1024, seed=23)
+    plan = ti.gemma4_fa4_mask(1, 1, 1024, q_offset=1024, kv_offset=1,
+                              attention_mask=torch.ones((1, 1025), dtype=torch.int32))
+    res = ti.gemma4_fa4_prepared(_module(LOCAL_LAYER), q, k, v, plan, **_kwargs(LOCAL_LAYER))
+    assert res.path == "fa4_local_varlen" and native[-1][1:5] == ([0, 1], [0, 1024], 1, 1024)
 
 
 def test_long_global_routes(native):
