@@ -20,6 +20,12 @@ events on the launch stream (the roofline of the dominant kernel), and the
 fp32 CPU oracle timed on this host (configuration 1 in full, forward-only and
 forward+backward of a bounded head sample of configuration 2).
 
+Also reported: the long-context row (configuration 6: one 65536-token global
+sequence, the reference's S64K row, 3 timed steps after 1 warm-up), and a
+measured bf16 GEMM rate (torch.matmul on 8192^3 random bf16 operands) as a
+second denominator beside the 2.5 PFLOP/s dense peak, as the reference divides
+by its measured GEMM rate (experiments/EXP-0029-h100-performance-baseline.md:70-71).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        [--no-extra]
 """
@@ -309,6 +315,20 @@ def kv_prep_timing(torch, dev, reps: int):
     return out
 
 
+def gemm_rate(torch, dev, reps: int = 10, n: int = 8192) -> float:
+    """Measured bf16 GEMM rate (TFLOP/s): torch.matmul of random n x n operands.
+
+    Random operands on purpose: the matrix core's power, and with it the
+    clock, depends on the data, so a GEMM of constant operands overstates what
+    the attention kernels' data allows.
+    """
+    g = torch.Generator(device=dev).manual_seed(8192)
+    a = torch.randn(n, n, generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn(n, n, generator=g, device=dev).to(torch.bfloat16)
+    ms = statistics.median(event_times(torch, lambda: torch.matmul(a, b), reps, 3))
+    return 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+
+
 def kernel_source_digest() -> str:
     """SHA-256 over the HIP sources, so recorded counters are tied to the kernels measured."""
     h = hashlib.sha256()
@@ -425,9 +445,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-extra", action="store_true",
                     help="only configuration 2 (skip configurations 1, 3, 4, 5 and the cold-cache run)")
-    ap.add_argument("--extra-configs", default="1,3,4,5",
+    ap.add_argument("--extra-configs", default="1,3,4,5,6",
                     help="comma-separated configurations timed besides configuration 2 "
-                         "(6: a 65536-token global sequence, on request only)")
+                         "(6: a 65536-token global sequence, at most 3 timed steps)")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache run")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -461,11 +481,18 @@ def main() -> int:
             del junk
         extra["kv_prep_global_S8192_4heads"] = kv_prep_timing(torch, dev, max(5, args.steps))
         chosen = [int(x) for x in args.extra_configs.split(",") if x.strip()]
-        for cfg in (getattr(wl, f"config{i}") for i in chosen if i != 2):
-            w = cfg()
-            extra[w.name], _ = run_workload(torch, g, w, steps=args.steps,
-                                            warmup=args.warmup, dev=dev)
+        for i in chosen:
+            if i == 2:
+                continue
+            w = getattr(wl, f"config{i}")()
+            long_ctx = i == 6  # about 0.75 s per forward+backward
+            extra[w.name], _ = run_workload(
+                torch, g, w, steps=min(args.steps, 3) if long_ctx else args.steps,
+                warmup=1 if long_ctx else args.warmup, dev=dev)
             torch.cuda.empty_cache()
+        gemm = gemm_rate(torch, dev)
+        extra["measured_bf16_gemm_tflops"] = round(gemm, 1)
+        extra["config2_fwd_bwd_pct_of_measured_gemm"] = round(100.0 * head["fwd_bwd_tflops"] / gemm, 2)
     value = head["fwd_bwd_tflops"]
     line = {
         "metric": "mask-aware TFLOP/s fwd/bwd (d256 sliding, d512 global, S=8192) + % bf16 MFMA peak",
