@@ -126,6 +126,12 @@ int g4_attn_fwd(const g4_problem* p,
  * G4_ERR_WORKSPACE.  Every call on a GPU uses the same array: calls that
  * overlap on one GPU (other streams, other threads) race; calls on one stream
  * are ordered and safe.  Allocates nothing, no host synchronisation.
+ * Under HIP graph capture: make one call on that GPU outside capture first
+ * (it looks up the array's address and sets the kernels' launch attributes);
+ * later calls record launches only.
+ * Cost: the array is part of the library's code object, so every process
+ * that loads the library holds 32 MiB of HBM on each GPU where its kernels
+ * are loaded, whether or not it calls this entry point.
  */
 #define G4_STATIC_WORKSPACE_BYTES (32u << 20)
 int g4_attn_fwd_static(const g4_problem* p,

@@ -95,3 +95,33 @@ def test_static_workspace_forward_matches_the_workspace_forward(make, first, sec
         assert torch.isfinite(o_ws.float()).all() and torch.isfinite(l_ws).all()
         assert torch.equal(o_ws, o_st), "O differs between the two entry points"
         assert torch.equal(l_ws, l_st), "LSE differs between the two entry points"
+
+
+def test_static_workspace_forward_replays_under_graph_capture():
+    # After one call outside capture (which looks up the array's address on
+    # this GPU and sets the kernels' launch attributes), g4_attn_fwd_static
+    # records into a HIP graph; every replay, with eager work and a
+    # synchronisation between replays, matches the eager g4_attn_fwd bit for bit.
+    from gemma4_fa4_amd import _lib
+    from gemma4_fa4_amd.attention import _layout
+
+    plan, q, k, v = _local_case(13, [900], [1100])  # vision spans live in the array
+    print("graph capture of g4_attn_fwd_static (local d256, vision + documents)", flush=True)
+    (o_ws, l_ws), _ = _both(plan, q, k, v)  # includes the static entry point's first call
+    lib = _lib.load()
+    prob = plan.problem()
+    o = torch.empty_like(q)
+    lse = torch.empty(plan.lse_shape(), dtype=torch.float32, device=DEV)
+    args = [ctypes.byref(prob), q.data_ptr(), _layout(q, True), k.data_ptr(), _layout(k, True),
+            v.data_ptr(), _layout(v, True), o.data_ptr(), _layout(o, True), lse.data_ptr()]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.g4_attn_fwd_static(*args, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc)
+    for _ in range(3):
+        o.fill_(float("nan"))
+        lse.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ws) and torch.equal(lse, l_ws)
