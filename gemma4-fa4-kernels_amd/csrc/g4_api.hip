@@ -91,7 +91,7 @@ int check_ws(const g4_problem* p, int phase, void* ws, size_t bytes) {
   } while (0)
 
 // Workspace: [spans][raise flags][document-pass list] (forward); backward adds
-// [delta][dS][queue counters][dQ recompute list]
+// [delta][dS][queue counters][dQ recompute list][dK / dV sums (striped)]
 size_t fwd_ws_bytes(const g4_problem& p) {
   return align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) + g4::fwd_doc_list_bytes(p);
 }
@@ -115,6 +115,10 @@ unsigned* sched_ptr(const g4_problem& p, void* ws) {
 int4* dq_list_ptr(const g4_problem& p, void* ws) {
   if (!g4::dq_list_bytes(p)) return nullptr;
   return (int4*)((char*)sched_ptr(p, ws) + g4::kSchedBytes);
+}
+float* acc_ptr(const g4_problem& p, void* ws) {
+  if (!g4::acc_bytes(p)) return nullptr;
+  return (float*)((char*)sched_ptr(p, ws) + g4::kSchedBytes + g4::dq_list_bytes(p));
 }
 
 // Forward workspace of g4_attn_fwd_static: a file-scope device array, one
@@ -234,15 +238,81 @@ void ds_geometry(const g4_problem& p, int* rows, int* cols) {
     *cols = (p.seqlen_k + 63) / 64;
   }
 }
-size_t ds_bytes(const g4_problem& p) {
-  const bool dense = p.head_dim == 512 && p.window == 0 &&
-                     !(p.vision_ids != nullptr && p.bidirectional_vision);
-  const bool band = p.head_dim == 256 && p.window > 0;
-  if (!dense && !band) return 0;
+static bool ds_dense_kind(const g4_problem& p) {
+  return p.head_dim == 512 && p.window == 0 && !(p.vision_ids != nullptr && p.bidirectional_vision);
+}
+static size_t ds_full_bytes(const g4_problem& p) {
   int rows, cols;
   ds_geometry(p, &rows, &cols);
-  const size_t b = (size_t)rows * cols * p.num_q_heads * 4096;
-  return b <= ds_cap(p) ? b : 0;
+  return (size_t)rows * cols * p.num_q_heads * 4096;
+}
+// fp32 dK and dV sums of the striped backward, over the K stream's tokens.
+static size_t sums_bytes(const g4_problem& p) {
+  return align256((size_t)2 * k_stream_tokens(p) * p.num_kv_heads * p.head_dim * 4);
+}
+// Striped stored dS: when the dense buffer of one causal head-dim 512 sequence
+// exceeds the budget, its 32-query rows are cut, from the first, into stripes
+// whose tiles (rows x the key tiles their last row reaches) fit the budget
+// less the fp32 dK / dV sums, each as many rows (a multiple of four) as fit.
+// The dK/dV launch of a stripe stores its dS and adds its dK / dV to the sums;
+// the dQ launch of the same stripe then reads those dS tiles.  Every (query,
+// key) pair is visited once by each stage, so nothing is recomputed.  Calls
+// f(stripe) in order; returns the number of stripes (0: not striped: the dense
+// layout fits, or the problem is not a single such sequence, or not even four
+// rows reaching every key tile fit).
+template <class F>
+static int for_each_ds_stripe(const g4_problem& p, F f) {
+  if (!ds_dense_kind(p) || p.num_seqs != 1) return 0;
+  const size_t budget = ds_cap(p);
+  if (budget == 0 || ds_full_bytes(p) <= budget || budget <= sums_bytes(p)) return 0;
+  const size_t cap = budget - sums_bytes(p);
+  const int64_t lq = p.seqlen_q, lk = p.seqlen_k;  // the one sequence's lengths
+  const int nrows = (int)((lq + 31) / 32);
+  const int ntk = (int)((lk + 63) / 64);
+  const int64_t off = lk - lq;
+  // key tiles the rows below r1 reach (their last query's causal end)
+  auto cols = [&](int r1) {
+    const int64_t last_q = std::min<int64_t>((int64_t)32 * r1, lq) - 1;
+    return (int)std::min<int64_t>(ntk, (last_q + off) / 64 + 1);
+  };
+  const size_t per = (size_t)p.num_q_heads * 4096;  // bytes per (row, key tile)
+  // Four rows that reach the last key tile must fit; then every stripe of
+  // four rows (or the fewer left at the end) does, as cols only grows.  The
+  // check comes before any f() call.
+  if ((size_t)4 * cols(nrows) * per > cap) return 0;
+  int n = 0;
+  for (int r0 = 0; r0 < nrows;) {
+    int h = std::min(4, nrows - r0);
+    while (r0 + h < nrows) {
+      const int h2 = std::min(h + 4, nrows - r0);
+      if ((size_t)h2 * cols(r0 + h2) * per > cap) break;
+      h = h2;
+    }
+    f(DsStripe{r0, h, cols(r0 + h)});
+    ++n;
+    r0 += h;
+  }
+  return n;
+}
+int ds_stripes(const g4_problem& p, DsStripe* out, int max_out) {
+  int i = 0;
+  return for_each_ds_stripe(p, [&](const DsStripe& s) {
+    if (i < max_out) out[i] = s;
+    ++i;
+  });
+}
+size_t acc_bytes(const g4_problem& p) { return ds_stripes(p, nullptr, 0) ? sums_bytes(p) : 0; }
+size_t ds_bytes(const g4_problem& p) {
+  const bool dense = ds_dense_kind(p);
+  const bool band = p.head_dim == 256 && p.window > 0;
+  if (!dense && !band) return 0;
+  const size_t b = ds_full_bytes(p);
+  if (b <= ds_cap(p)) return b;
+  size_t most = 0;  // the largest stripe, when striped
+  for_each_ds_stripe(p, [&](const DsStripe& s) {
+    most = std::max(most, (size_t)s.rows * s.cols * p.num_q_heads * 4096);
+  });
+  return most;
 }
 // Head dim 256 stored-dS dQ with vision IDs: one 16-byte entry per possible
 // (sequence, 128-query tile, query head) for the tiles left to recompute.
@@ -278,7 +348,8 @@ size_t g4_workspace_bytes(const g4_problem* p, int phase) {
   if (check_problem(p) != G4_OK) return 0;
   size_t b = fwd_ws_bytes(*p);
   if (phase == 1)
-    b += g4::delta_bytes(*p) + g4::ds_bytes(*p) + g4::kSchedBytes + g4::dq_list_bytes(*p);
+    b += g4::delta_bytes(*p) + g4::ds_bytes(*p) + g4::kSchedBytes + g4::dq_list_bytes(*p) +
+         g4::acc_bytes(*p);
   return b;
 }
 
@@ -318,7 +389,10 @@ static int fill_bwd(g4::BwdParams& a, const g4_problem* p, const void* q, g4_lay
   a.vl = vl;
   a.num_seqs = p->num_seqs;
   a.delta = delta_ptr(*p, ws);
-  a.ds = ds_ptr(*p, ws);
+  // A striped problem's dS buffer holds one stripe at a time, which only
+  // g4_attn_bwd interleaves with the dQ launches; the separate stage entry
+  // points run it without stored dS (the dQ stage recomputes S and dP).
+  a.ds = g4::ds_stripes(*p, nullptr, 0) ? nullptr : ds_ptr(*p, ws);
   g4::ds_geometry(*p, &a.ds_rows, &a.ds_cols);
   a.sched = sched_ptr(*p, ws);
   a.dq_list = dq_list_ptr(*p, ws);
@@ -411,10 +485,57 @@ int g4_attn_bwd(const g4_problem* p, const void* q, g4_layout ql, const void* k,
                 void* dk, g4_layout dkl, void* dv, g4_layout dvl, void* ws, size_t ws_bytes,
                 void* stream) {
   G4_TRY(g4_attn_bwd_delta(p, o, ol, dout, dol, dlse, ws, ws_bytes, stream));
-  G4_TRY(g4_attn_bwd_dkdv(p, q, ql, k, kl, v, vl, dout, dol, lse, dk, dkl, dv, dvl, ws, ws_bytes,
-                          stream));
-  G4_TRY(g4_attn_bwd_dq(p, q, ql, k, kl, v, vl, dout, dol, lse, dq, dql, ws, ws_bytes, stream));
-  return G4_OK;
+  const int nstripes = g4::ds_stripes(*p, nullptr, 0);
+  if (nstripes == 0) {
+    G4_TRY(g4_attn_bwd_dkdv(p, q, ql, k, kl, v, vl, dout, dol, lse, dk, dkl, dv, dvl, ws,
+                            ws_bytes, stream));
+    G4_TRY(g4_attn_bwd_dq(p, q, ql, k, kl, v, vl, dout, dol, lse, dq, dql, ws, ws_bytes, stream));
+    return G4_OK;
+  }
+  // Striped stored dS (g4::for_each_ds_stripe): per stripe, the dK/dV launch
+  // (which stores the stripe's dS and adds to the fp32 dK / dV sums) then the
+  // dQ launch that reads them, all on the one stream.
+  G4_TRY(check_operand(q, ql, "q"));
+  G4_TRY(check_operand(k, kl, "k"));
+  G4_TRY(check_operand(v, vl, "v"));
+  G4_TRY(check_operand(dout, dol, "dout"));
+  G4_TRY(check_operand(dq, dql, "dq"));
+  G4_TRY(check_operand(dk, dkl, "dk"));
+  G4_TRY(check_operand(dv, dvl, "dv"));
+  if (lse == nullptr) return fail(G4_ERR_INVALID, "lse is NULL");
+  g4::BwdParams a{};
+  fill_bwd(a, p, q, ql, k, kl, v, vl, ws);
+  a.ds = ds_ptr(*p, ws);
+  a.dout = (const __bf16*)dout;
+  a.dol = dol;
+  a.lse = lse;
+  a.dq = (__bf16*)dq;
+  a.dql = dql;
+  a.dk = (__bf16*)dk;
+  a.dv = (__bf16*)dv;
+  a.dkl = dkl;
+  a.dvl = dvl;
+  a.dk_acc = acc_ptr(*p, ws);
+  a.dv_acc = a.dk_acc + (size_t)g4::k_stream_tokens(*p) * p->num_kv_heads * p->head_dim;
+  hipStream_t st = (hipStream_t)stream;
+  int i = 0, rc = G4_OK;
+  g4::for_each_ds_stripe(*p, [&](const g4::DsStripe& s) {
+    if (rc != G4_OK) return;
+    a.ds_row_lo = s.row_lo;
+    a.ds_rows = s.rows;
+    a.ds_cols = s.cols;
+    a.dq_qt_lo = s.row_lo / 4;
+    a.acc_mode = (i > 0 ? 1 : 0) | (i + 1 == nstripes ? 2 : 0);
+    hipError_t e = g4::launch_bwd_dkdv(a, st);
+    if (e != hipSuccess) {
+      rc = hip_fail(e, "backward dK/dV (striped)");
+      return;
+    }
+    e = g4::launch_bwd_dq(a, st);
+    if (e != hipSuccess) rc = hip_fail(e, "backward dQ (striped)");
+    ++i;
+  });
+  return rc;
 }
 
 int g4_mask_materialize(const g4_problem* p, uint8_t* out, void* ws, size_t ws_bytes,

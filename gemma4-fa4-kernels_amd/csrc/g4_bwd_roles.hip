@@ -113,7 +113,8 @@ struct RolesCfg {
 };
 
 // ROT: the dh = 1 P waves read the Q tile rotated by 16 rows (see step_p).
-template <bool META, bool ROT>
+// STRIPED: one stripe of the striped stored-dS backward (BwdParams::ds_row_lo).
+template <bool META, bool ROT, bool STRIPED>
 struct RolesKernel {
   using C = RolesCfg;
   char G4_LDS* smem;
@@ -387,27 +388,42 @@ struct RolesKernel {
                               (int64_t)kvh * a->dvl.head_stride
                         : a->dk + tok_off(sq, s, sq.ktok, my_j, a->dkl) +
                               (int64_t)kvh * a->dkl.head_stride;
+    // Striped: add to / write the fp32 sums over the stripes; the last stripe
+    // writes bf16 dK / dV (see BwdParams::acc_mode).  A middle stripe without
+    // steps for this tile leaves its sums as they are.
+    float* sum = nullptr;
+    if constexpr (STRIPED) {
+      if (nsteps == 0 && a->acc_mode == 1) return;
+      sum = (PWAVE ? a->dv_acc : a->dk_acc) +
+            ((sq.ktok + my_j) * a->p.num_kv_heads + kvh) * (int64_t)C::D;
+    }
 #pragma unroll
     for (int b = 0; b < C::kNB; ++b)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int d = dh * C::kDH + b * 32 + 8 * r4 + 4 * h32;
-        const f32x16& x = acc[b];
-        *(bf16x4*)(dst + d) = bf16x4{(__bf16)x[r4 * 4], (__bf16)x[r4 * 4 + 1],
-                                     (__bf16)x[r4 * 4 + 2], (__bf16)x[r4 * 4 + 3]};
+        f32x4 x = f32x4{acc[b][r4 * 4], acc[b][r4 * 4 + 1], acc[b][r4 * 4 + 2], acc[b][r4 * 4 + 3]};
+        if (STRIPED) {
+          if (a->acc_mode & 1) x += *(const f32x4*)(sum + d);
+          if (!(a->acc_mode & 2)) {
+            *(f32x4*)(sum + d) = x;
+            continue;
+          }
+        }
+        *(bf16x4*)(dst + d) = bf16x4{(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]};
       }
   }
 };
 
 // One key tile kt of sequence s and KV head kvh; its query tiles are walked
 // upward with `up`, else from the last one down.
-template <bool META, bool QUEUE>
+template <bool META, bool QUEUE, bool STRIPED>
 __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_raw, int kvh,
                                                 int s, int kt, bool up) {
   // Rotation only in the one-item-per-workgroup launch: measured on config 2
   // (one 8192-token sequence) dK/dV 5.32 -> 5.17 ms, but 5.21 -> 5.89 ms in the
   // work-queue launch of config 4 (packed, 1-2048-token segments).
-  using K = RolesKernel<META, !QUEUE>;
+  using K = RolesKernel<META, !QUEUE, STRIPED>;
   using C = RolesCfg;
   K ker;
   ker.smem = (char G4_LDS*)smem_raw;
@@ -466,8 +482,19 @@ __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_r
     ker.has_doc = false;
     ker.has_meta = ker.has_vid;
   }
+  if constexpr (STRIPED) {
+    // Striped (one sequence): only the stripe's rows, query tiles (one 32-query
+    // row each) [ds_row_lo, ds_row_lo + ds_rows) of the sequence, stored from
+    // the buffer's first row.
+    const int lo = max(ker.qt_lo, a.ds_row_lo);
+    const int hi = min(ker.qt_lo + ker.nqt, a.ds_row_lo + a.ds_rows);
+    ker.qt_lo = lo;
+    ker.nqt = max(hi - lo, 0);
+    ker.ds_row0 = -a.ds_row_lo;
+  } else {
+    ker.ds_row0 = sq.packed ? sq.qtok / 32 + ker.s : (int64_t)ker.s * ((p.seqlen_q + 31) / 32);
+  }
   const int nsteps = ker.nqt * ker.grp;
-  ker.ds_row0 = sq.packed ? sq.qtok / 32 + ker.s : (int64_t)ker.s * ((p.seqlen_q + 31) / 32);
   ker.ds_lane = (ker.kb * 32 + (ker.lane & 31)) * 64 + 32 * ker.dh + 8 * ker.h32;
   const int jc = min(ker.my_j, sq.lk - 1);
   ker.my_vid = ker.has_vid ? p.vision_ids[sq.ktok + jc] : -1;
@@ -513,7 +540,7 @@ __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_r
 // sequences): only the pairs that exist, sequence by sequence from the longest
 // (a pair's cost grows with its sequence's length, and a longer sequence has
 // more pairs: the heaviest items go first), then KV head, then pair.
-template <bool META, bool QUEUE>
+template <bool META, bool QUEUE, bool STRIPED>
 __device__ __forceinline__ void dkdv_roles_pair(const BwdParams& a, char* smem_raw, int L,
                                                 bool by_length = false) {
   using C = RolesCfg;
@@ -542,14 +569,14 @@ __device__ __forceinline__ void dkdv_roles_pair(const BwdParams& a, char* smem_r
       if (kt == r) break;
       barrier_lds();  // every wave is done with the first tile's LDS
     }
-    dkdv_roles_tile<META, QUEUE>(a, smem_raw, kvh, s, kt, pass == 1);
+    dkdv_roles_tile<META, QUEUE, STRIPED>(a, smem_raw, kvh, s, kt, pass == 1);
   }
 }
 
 // Persistent: a few workgroups per CU take pair tickets from the dK/dV work
 // queue.  (With one workgroup per key tile, per-CU busy time on an 8192-token
 // causal sequence ranged from 8% to 100% of the launch.)
-template <bool META, bool QUEUE>
+template <bool META, bool QUEUE, bool STRIPED>
 __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams a) {
   extern __shared__ __attribute__((aligned(16))) char smem_raw[];
   if constexpr (QUEUE) {
@@ -571,10 +598,10 @@ __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams 
     for (;;) {
       const int t = wq.next((int G4_LDS*)smem_raw);
       if (t >= n) break;
-      dkdv_roles_pair<META, true>(a, smem_raw, t, by_length);
+      dkdv_roles_pair<META, true, STRIPED>(a, smem_raw, t, by_length);
     }
   } else {
-    dkdv_roles_pair<META, false>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
+    dkdv_roles_pair<META, false, STRIPED>(a, smem_raw, xcd_remap(blockIdx.x, gridDim.x));
   }
 }
 
@@ -1736,7 +1763,7 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
     qh = L % hslots * ker.nh;
   } else {
     const int per_qt = a.num_seqs * hslots;
-    qt = a.ntiles - 1 - L / per_qt;
+    qt = a.dq_qt_lo + a.ntiles - 1 - L / per_qt;
     const int rem = L % per_qt;
     s = rem / hslots;
     qh = rem % hslots * ker.nh;
@@ -1785,8 +1812,11 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
 
   ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
   ker.kstride = a.kl.token_stride;
+  // (striped: the stripe's rows of the one sequence, from the buffer's first)
   const int64_t row0 =
-      (sq.packed ? sq.qtok / 32 + s : (int64_t)s * ((p.seqlen_q + 31) / 32)) + i0 / 32;
+      (a.dk_acc != nullptr ? -(int64_t)a.ds_row_lo
+                           : sq.packed ? sq.qtok / 32 + s : (int64_t)s * ((p.seqlen_q + 31) / 32)) +
+      i0 / 32;
   ker.ds_head_stride = (int64_t)a.ds_rows * a.ds_cols * 4096;
   if constexpr (kBand) {
     ker.ds_col_stride = 4096;
@@ -1905,7 +1935,8 @@ static hipError_t launch_dq_ds(const BwdParams& a, hipStream_t stream) {
   using C = DqDsCfg<D>;
   static LdsAttr attr[2];
   BwdParams b = a;
-  b.ntiles = (a.p.seqlen_q + C::kBM - 1) / C::kBM;
+  // (striped: the stripe's 128-query tiles, from dq_qt_lo)
+  b.ntiles = a.dk_acc != nullptr ? (a.ds_rows + 3) / 4 : (a.p.seqlen_q + C::kBM - 1) / C::kBM;
   const int64_t items =
       (int64_t)b.num_seqs * b.ntiles * (a.p.num_q_heads / dq_ds_heads<D>(a.p));
   if (items <= 0) return hipSuccess;
@@ -1996,11 +2027,19 @@ hipError_t launch_dkdv_roles_d(const BwdParams& a, hipStream_t stream) {
   if (items <= 0) return hipSuccess;
   void (*kq[2])(BwdParams);  // [meta] queue variants
   void (*ks[2])(BwdParams);  // [meta] one workgroup per item
+  const bool striped = D == 512 && a.dk_acc != nullptr;
   if constexpr (D == 512) {
-    kq[0] = dkdv_roles_kernel<false, true>;
-    kq[1] = dkdv_roles_kernel<true, true>;
-    ks[0] = dkdv_roles_kernel<false, false>;
-    ks[1] = dkdv_roles_kernel<true, false>;
+    if (striped) {
+      kq[0] = dkdv_roles_kernel<false, true, true>;
+      kq[1] = dkdv_roles_kernel<true, true, true>;
+      ks[0] = dkdv_roles_kernel<false, false, true>;
+      ks[1] = dkdv_roles_kernel<true, false, true>;
+    } else {
+      kq[0] = dkdv_roles_kernel<false, true, false>;
+      kq[1] = dkdv_roles_kernel<true, true, false>;
+      ks[0] = dkdv_roles_kernel<false, false, false>;
+      ks[1] = dkdv_roles_kernel<true, false, false>;
+    }
   } else {
     kq[0] = dkdv_roles256_kernel<false, true>;
     kq[1] = dkdv_roles256_kernel<true, true>;
@@ -2012,8 +2051,8 @@ hipError_t launch_dkdv_roles_d(const BwdParams& a, hipStream_t stream) {
   const int64_t nblocks = grid.size((const void*)kq[meta], C::kNT, C::kLdsBytes, items, &queue);
   if (nblocks <= 0) return hipErrorInvalidValue;
   void (*kern)(BwdParams) = queue ? kq[meta] : ks[meta];
-  static LdsAttr attr[4];
-  hipError_t e = attr[2 * meta + queue].ensure((const void*)kern, C::kLdsBytes);
+  static LdsAttr attr[8];
+  hipError_t e = attr[4 * striped + 2 * meta + queue].ensure((const void*)kern, C::kLdsBytes);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(C::kNT), C::kLdsBytes, stream, b);
   return hipGetLastError();

@@ -74,6 +74,18 @@ struct BwdParams {
   // order, so each lane stores one 32-byte run).
   __bf16* ds;
   int ds_rows, ds_cols;
+  // Striped stored-dS backward (head dim 512, one causal sequence whose dense
+  // dS exceeds the budget; see DsStripe): the buffer holds rows
+  // [ds_row_lo, ds_row_lo + ds_rows) of this launch's stripe, and the dQ
+  // launch takes the stripe's 128-query tiles from dq_qt_lo.  0 otherwise.
+  int ds_row_lo, dq_qt_lo;
+  // fp32 dK / dV sums over the stripes ((Tk, Hkv, D), null unless striped) and
+  // what the dK/dV launch's epilogue does with them: bit 0 adds the stored
+  // sums (every stripe after the first), bit 1 writes the bf16 dK / dV (the
+  // last stripe), else the fp32 sums are written.
+  float* dk_acc;
+  float* dv_acc;
+  int acc_mode;
   // Head dim 256 dQ after the stored-dS pass: only the query tiles whose vision
   // spans reach past the stored band (set by the launcher).
   int dq_recompute_only;
@@ -151,6 +163,18 @@ struct PersistentGrid {
 // dS buffer of the head-dim 512 causal backward (0: the dQ stage recomputes S, dP).
 size_t ds_bytes(const g4_problem& p);
 void ds_geometry(const g4_problem& p, int* rows, int* cols);
+// A stripe of the striped stored-dS backward: 32-query rows [row_lo, row_lo +
+// rows) (rows a multiple of 4, so stripes hold whole 128-query dQ tiles) and the
+// key tiles they reach (cols).
+struct DsStripe {
+  int row_lo, rows, cols;
+};
+// Stripes of a problem whose dense dS exceeds its budget: one causal head-dim
+// 512 sequence whose rows fit in stripes of at least four rows; writes up to
+// max_out of them and returns how many there are (0: not striped).
+int ds_stripes(const g4_problem& p, DsStripe* out, int max_out);
+// fp32 dK / dV sums of the striped backward (0 when not striped).
+size_t acc_bytes(const g4_problem& p);
 int64_t k_stream_tokens(const g4_problem& p);
 int64_t q_stream_tokens(const g4_problem& p);
 

@@ -754,8 +754,11 @@ def _fit_ds_budget(plan: _Plan, q, k, v, budget: int) -> int:
     (transformers_integration.py:1950-1961, which re-runs a low-memory
     composition when the native global backward exceeds its budget): the
     dK/dV stage stores dS tiles only while they fit what the budget leaves after
-    the gradients and the O(T) part of the workspace; past that the dQ stage
-    recomputes S and dP.  Returns the additional bytes the backward will need.
+    the gradients and the O(T) part of the workspace.  Past that, a single
+    global sequence is cut into stripes of query rows that fit it (with fp32
+    dK / dV sums beside them); other problems, and budgets below the sums plus
+    four rows of tiles, have the dQ stage recompute S and dP.  Returns the
+    additional bytes the backward will need.
     """
     plan.ds_budget = 0
     full = _backward_additional_bytes(plan, q, k, v)
@@ -778,12 +781,14 @@ def pin_backward_ds_budget(nbytes: int | None) -> int | None:
     """Pin the backward's stored-dS budget for every later call; returns the previous pin.
 
     ``None`` (the default) fits the budget to the free HBM at each forward and
-    again at each backward: the dK/dV stage stores dS tiles while they fit, else
-    the dQ stage recomputes S and dP.  The two routes sum dQ in different
-    orders, so with the default the bits of dQ can depend on how much HBM is
-    free.  A pinned budget fixes the route: a negative value always
-    recomputes, a positive one stores the tiles that fit in that many bytes, 0
-    is the library's default cap (16 GiB).  The global layers still raise
+    again at each backward: the dK/dV stage stores dS tiles while they fit, a
+    single global sequence past that is striped, else the dQ stage recomputes S
+    and dP.  The recompute route sums dQ in another order, and the striped
+    route adds dK / dV over its stripes in fp32, so with the default the bits of
+    the gradients can depend on how much HBM is free.  A pinned budget fixes the
+    route: a negative value always recomputes, a positive one stores the tiles
+    (or stripes) that fit in that many bytes, 0 is the library's default cap
+    (16 GiB).  The global layers still raise
     ``GlobalBackwardBudgetExceeded`` when the pinned route does not fit the
     guarded budget.  A process-wide setting (not per thread).
     """

@@ -137,6 +137,17 @@ class Stages:
             self.dk.data_ptr(), L["dk"], self.dv.data_ptr(), L["dv"], self.ws.data_ptr(),
             self.ws.numel(), self._stream()))
 
+    def backward(self):
+        """The whole backward through g4_attn_bwd (delta, then dK/dV and dQ; a
+        striped problem interleaves the two per stripe)."""
+        L = self.lay
+        _lib.check(self.lib.g4_attn_bwd(
+            ctypes.byref(self.prob), self.q.data_ptr(), L["q"], self.k.data_ptr(), L["k"],
+            self.v.data_ptr(), L["v"], self.o.data_ptr(), L["o"], self.dout.data_ptr(), L["do"],
+            self.lse.data_ptr(), None if self.dlse is None else self.dlse.data_ptr(),
+            self.dq.data_ptr(), L["dq"], self.dk.data_ptr(), L["dk"], self.dv.data_ptr(),
+            L["dv"], self.ws.data_ptr(), self.ws.numel(), self._stream()))
+
     def dq_stage(self):
         L = self.lay
         _lib.check(self.lib.g4_attn_bwd_dq(

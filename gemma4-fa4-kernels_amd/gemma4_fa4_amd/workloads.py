@@ -142,8 +142,8 @@ def config5(seed: int = 5) -> Workload:
 def config6(seed: int = 6) -> Workload:
     """Long context (not a BASELINE configuration): one global d512 causal sequence of
     65536 tokens, the reference's S64K row (EXP-0035:69-70).  Its dense stored-dS
-    buffer (256 GiB) exceeds the default budget, so the backward recomputes S and dP
-    in the dQ stage."""
+    buffer (256 GiB) exceeds the default budget, so the backward stores dS stripe by
+    stripe (ten stripes of query rows within the 16 GiB default)."""
     return Workload("config6_global_d512_S65536_fwd_bwd", "global", [65536],
                     ("fwd", "bwd", "fwd_bwd"), seed=seed, device_rng=True)
 

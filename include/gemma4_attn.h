@@ -74,9 +74,11 @@ typedef struct g4_problem {
   int64_t lse_head_stride;
   /* Bytes of the backward workspace that may hold dS tiles stored by the
    * dK/dV stage for the dQ stage: 0 = the library default (16 GiB), < 0 =
-   * none.  When the tiles a problem needs exceed the budget, none are stored
-   * and the dQ stage recomputes S and dP (slower, workspace O(T) instead of
-   * O(T * Sk)).  Results are the same either way up to fp32 summation order.
+   * none.  When the tiles a problem needs exceed the budget, g4_attn_bwd
+   * stripes a single head-dim 512 causal sequence (see g4_attn_bwd); in every
+   * other case none are stored and the dQ stage recomputes S and dP (slower,
+   * workspace O(T) instead of O(T * Sk)).  Results are the same on every
+   * route up to fp32 summation order.
    * The reference's global backward budget policy is the analogous knob
    * (src/gemma4_fa4/h100.py:713-746). */
   int64_t ds_budget;
@@ -146,6 +148,14 @@ int g4_attn_fwd_static(const g4_problem* p,
  * Backward: dQ, dK, dV given O, dO, LSE and optional dLSE (same layout as LSE,
  * NULL = zero).  dK and dV are distinct outputs; no atomics (bitwise
  * repeatable).  Runs g4_attn_bwd_delta, g4_attn_bwd_dkdv and g4_attn_bwd_dq.
+ * Striped route: a problem of one head-dim 512 causal sequence whose dense dS
+ * tiles exceed ds_budget is cut into stripes of 32-query rows, each stripe's
+ * tiles fitting the budget beside fp32 dK / dV sums (2 x K tokens x KV heads
+ * x 512 x 4 bytes, counted in the budget and in g4_workspace_bytes); the
+ * dK/dV and dQ launches then alternate per stripe, so nothing is recomputed.
+ * dQ is then bitwise that of the dense stored route; dK and dV differ from it
+ * by the fp32 additions between stripes.  (The three stage entry points on
+ * such a problem take the recompute route instead.)
  * Replaces FA4's autograd backward (local) and the patched global d512
  * orchestrator _flash_attn_bwd_gemma4_global_d512
  * (patches/flash-attention/0002-*.patch:1021-1512, called from

@@ -1,16 +1,16 @@
 """C-ABI parity of the backward without stored dS tiles (the dQ stage recomputes S and dP).
 
 The dK/dV stage stores bf16 dS tiles for the dQ stage while they fit the
-problem's ``ds_budget`` (16 GiB by default).  Past it -- a single global
-sequence longer than 16384 tokens, or packed global batches whose rows times
-longest segment pass the budget -- the dK/dV kernels run their store-less
-branch and dQ comes from the recomputing role kernels (``dq_roles_kernel``
-at head dim 512, ``dq_roles256_kernel`` at 256).  A negative budget forces
-that route at small sizes; every case is checked against the fp64 oracle with
-the reference's M1 envelopes, and against the stored-dS route.  The last test
-runs a real 16448-token global sequence through the packed adapter with the
-default budget (the route the reference's S=64K measurement takes,
-experiments/EXP-0035-h100-global-dq-d256-streaming.md:69-70).
+problem's ``ds_budget`` (16 GiB by default).  Past it -- packed global batches
+whose rows times longest segment pass the budget, local bands that do not fit,
+and the separate stage entry points of a single global sequence that
+``g4_attn_bwd`` would stripe -- the dK/dV kernels run their store-less branch
+and dQ comes from the recomputing role kernels (``dq_roles_kernel`` at head
+dim 512, ``dq_roles256_kernel`` at 256).  A negative budget forces that route
+at small sizes; every case is checked against the fp64 oracle with the
+reference's M1 envelopes, and against the stored-dS route.  (A single global
+sequence past the budget takes the striped stored-dS route of g4_attn_bwd,
+tested on its own.)
 """
 
 import pytest
@@ -170,37 +170,3 @@ def test_d256_listed_recompute_past_255_query_heads():
     check_gradients([got[2][:, heads], got[3][:, kvs], got[4][:, kvs]],
                     [dq_ref[:, heads], dk_ref[:, kvs], dv_ref[:, kvs]],
                     [bq[:, heads], bk[:, kvs], bv[:, kvs]], label=label)
-
-
-def test_global_sequence_past_the_default_ds_budget():
-    import gemma4_fa4_amd as g
-
-    s = 16448  # 514 rows x 257 key tiles x 32 heads x 4 KB > 16 GiB: no stored dS
-    print(f"global S={s} through fa4_global_varlen_forward", flush=True)
-    gen = torch.Generator(device=DEV).manual_seed(16448)
-    sd = 512 ** -0.25
-    q = (torch.randn(s, 32, 512, generator=gen, device=DEV) * sd).to(torch.bfloat16)
-    k = (torch.randn(s, 4, 512, generator=gen, device=DEV) * sd).to(torch.bfloat16)
-    v = torch.randn(s, 4, 512, generator=gen, device=DEV).to(torch.bfloat16)
-    do = torch.randn(s, 32, 512, generator=gen, device=DEV).to(torch.bfloat16)
-    c = torch.tensor([0, s], dtype=torch.int32, device=DEV)
-    qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
-    o, lse = g.fa4_global_varlen_forward(qd, kd, vd, c, c, max_seqlen_q=s, max_seqlen_k=s)
-    torch.autograd.backward(o, do)
-    torch.cuda.synchronize()
-    from gemma4_fa4_amd.attention import _packed_plan
-
-    plan = _packed_plan(q, k, c, c, s, s, g.GLOBAL_ATTENTION)
-    assert _workspace_has_no_ds(plan)
-    heads = list(range(8, 16))  # KV group 1 in full, so its dK/dV are complete
-    cc = [0, s]
-    o_ref, l_ref, dq_ref, dk_ref, dv_ref = attention_fwd_bwd(
-        q, k, v, cc, cc, do=do, compute_dtype=torch.float64, heads=heads, q_chunk=1024)
-    _, bq, bk, bv = bf16_baseline_fwd_bwd(q, k, v, cc, cc, do=do, heads=heads, q_chunk=512)
-    h = slice(8, 16)
-    check_forward(o.detach()[:, h], lse.detach()[h], o_ref[:, h].cpu(), l_ref[h].cpu(),
-                  local=False, label="S16448")
-    check_gradients(
-        [qd.grad[:, h], kd.grad[:, 1:2], vd.grad[:, 1:2]],
-        [dq_ref[:, h].cpu(), dk_ref[:, 1:2].cpu(), dv_ref[:, 1:2].cpu()],
-        [bq[:, h].cpu(), bk[:, 1:2].cpu(), bv[:, 1:2].cpu()], label="S16448")

@@ -78,19 +78,47 @@ def test_ds_budget_sizes_the_stored_dS_tiles():
     dense = 128 * 64 * 32 * 4096
     assert _ws(**d512) - _ws(**d512, ds_budget=-1) == dense
     assert _ws(**d512, ds_budget=dense) - _ws(**d512, ds_budget=-1) == dense
-    assert _ws(**d512, ds_budget=dense - 1) == _ws(**d512, ds_budget=-1)
+    # Past the budget the one sequence is striped: fp32 dK / dV sums (2 x 4096
+    # keys x 4 KV heads x 512 x 4 B) plus the largest stripe must fit it.  With
+    # room for 2048 (row, key tile) units of 32 x 4 KB after the sums, rows
+    # [0, 64) reach 32 key tiles (64 x 32 = 2048 units), rows [64, 100) reach
+    # 50 (1800; 40 rows would need 40 x 52 = 2080), rows [100, 128) all 64 (1792).
+    sums = 2 * 4096 * 4 * 512 * 4
+    unit = 32 * 4096
+    budget = sums + 2048 * unit
+    assert _ws(**d512, ds_budget=budget) - _ws(**d512, ds_budget=-1) == sums + 2048 * unit
+    # one byte less: rows [0, 60) x 30 key tiles (1800), rows [60, 100) x 50
+    # (2000; 44 rows would need 44 x 52), rows [100, 128) x 64 (1792)
+    assert _ws(**d512, ds_budget=budget - 1) - _ws(**d512, ds_budget=-1) == sums + 2000 * unit
+    # the last four rows reach all 64 key tiles: below 4 x 64 units after the
+    # sums nothing is stored (the dQ stage recomputes); at it, stripes of at
+    # most 256 units
+    assert _ws(**d512, ds_budget=sums + 4 * 64 * unit - 1) == _ws(**d512, ds_budget=-1)
+    assert _ws(**d512, ds_budget=sums + 4 * 64 * unit) - _ws(**d512, ds_budget=-1) == (
+        sums + 256 * unit)
     # head dim 256 window 1024: a band of (1024 + 30) // 64 + 2 = 18 key tiles per row
     d256 = dict(seqlen_q=4096, seqlen_k=4096, num_kv_heads=16, head_dim=256, window=1024)
     band = 128 * 18 * 32 * 4096
     assert _ws(**d256) - _ws(**d256, ds_budget=-1) == band
     assert _ws(**d256, ds_budget=band - 1) == _ws(**d256, ds_budget=-1)
     # the default budget is 16 GiB: exactly a 16384-token global sequence's tiles;
-    # one more 32-query row and none are stored
+    # one more 32-query row and the sequence is striped within the 16 GiB
     at = dict(seqlen_q=16384, seqlen_k=16384, num_kv_heads=4, head_dim=512, window=0)
     assert _ws(**at) - _ws(**at, ds_budget=-1) == 16 << 30
     big = dict(seqlen_q=16416, seqlen_k=16416, num_kv_heads=4, head_dim=512, window=0)
-    assert _ws(**big) == _ws(**big, ds_budget=-1)
+    striped = _ws(**big) - _ws(**big, ds_budget=-1)
+    big_sums = 2 * 16416 * 4 * 512 * 4
+    assert big_sums < striped <= 16 << 30 and (striped - big_sums) % unit == 0
     assert _ws(**big, ds_budget=1 << 36) - _ws(**big, ds_budget=-1) == 513 * 257 * 32 * 4096
+    # a packed batch is never striped: past the budget its dQ stage recomputes
+    two = dict(num_kv_heads=4, head_dim=512, window=0)
+    p2 = _lib.G4Problem(num_seqs=2, num_q_heads=32, seqlen_q=4096, seqlen_k=4096, **two)
+    import ctypes
+    lib = _lib.load()
+    p2.ds_budget = -1
+    lean = lib.g4_workspace_bytes(ctypes.byref(p2), 1)
+    p2.ds_budget = budget
+    assert lib.g4_workspace_bytes(ctypes.byref(p2), 1) == lean
 
 
 @pytest.mark.parametrize("make,ok", [
@@ -336,8 +364,10 @@ def test_static_workspace_forward_rejects_a_problem_beyond_its_array():
 def test_backward_budget_drops_stored_ds_before_failing(monkeypatch):
     # The dS tiles are stored only while gradients + workspace fit the
     # reference's budget (80% of free HBM, at most free - 2 GiB); past it the
-    # dQ stage recomputes (lean workspace); only when even that does not fit
-    # is GlobalBackwardBudgetExceeded raised (h100.py:713-746 policy).
+    # one sequence is striped within what is left, and below the fp32 sums plus
+    # four rows of tiles the dQ stage recomputes (lean workspace); only when
+    # even that does not fit is GlobalBackwardBudgetExceeded raised
+    # (h100.py:713-746 policy).
     s = 4096
     q = torch.empty(s, 32, 512, dtype=torch.bfloat16)
     k = torch.empty(s, 4, 512, dtype=torch.bfloat16)
@@ -358,6 +388,13 @@ def test_backward_budget_drops_stored_ds_before_failing(monkeypatch):
     att._preflight_backward(plan, q, k, v)
     assert plan.ds_budget == 0  # everything fits: default budget, tiles stored
     monkeypatch.setattr(att, "_free_hbm", lambda _d: free_for(full - 1))
+    att._preflight_backward(plan, q, k, v)
+    assert plan.ds_budget > 0 and lean < att._backward_additional_bytes(plan, q, k, v) < full
+    sums, last_rows = 2 * s * 4 * 512 * 4, 4 * 64 * 32 * 4096
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: free_for(lean + sums + last_rows))
+    att._preflight_backward(plan, q, k, v)
+    assert att._backward_additional_bytes(plan, q, k, v) == lean + sums + last_rows
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: free_for(lean + sums + last_rows - 1))
     att._preflight_backward(plan, q, k, v)
     assert plan.ds_budget > 0 and att._backward_additional_bytes(plan, q, k, v) == lean
     monkeypatch.setattr(att, "_free_hbm", lambda _d: free_for(lean - 1))
