@@ -37,7 +37,7 @@ __global__ void __launch_bounds__(256) delta_kernel(BwdParams a, int64_t tq) {
   const int64_t items = tq * groups;
   const int c = lane % CPR, hl = lane / CPR;
   // Every backward call starts its tile kernels' work queues from zero.
-  if (blockIdx.x == 0 && threadIdx.x < 4 && a.sched != nullptr) a.sched[threadIdx.x] = 0u;
+  if (blockIdx.x == 0 && threadIdx.x < kSchedClear && a.sched != nullptr) a.sched[threadIdx.x] = 0u;
   for (int64_t r = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) / 64; r < items;
        r += (int64_t)gridDim.x * blockDim.x / 64) {
     const int64_t t = r / groups;

@@ -614,6 +614,58 @@ struct PrefetchQueue {
   }
 };
 
+// Work queue split over the eight XCDs, for items whose neighbours share
+// operands: item range [c n / 8, (c + 1) n / 8) belongs to XCD c, and the
+// workgroups of XCD c (blockIdx.x % 8 under the round-robin dispatch that
+// xcd_remap also assumes) draw it in order from counter c, so neighbouring
+// items run at the same time on the workgroups that share one L2.  A
+// workgroup whose range is exhausted draws from the next XCD's (c + 1, ...),
+// which only happens at the end of the launch.  Counters: ctr[0..7] per range,
+// ctr[8] counts the workgroups that finished; the last one zeroes all nine for
+// the next launch on the same workspace (the first relies on them being
+// zero).  Thread 0 draws the next ticket while the current item runs:
+//   XcdQueue q{ctr, n}; q.draw();
+//   for (int t = q.next(slot); t >= 0; t = q.next(slot)) { q.draw(); item(t); }
+// (no tile copy may be in flight into the LDS slot at next()).
+struct XcdQueue {
+  static constexpr int kXcd = 8;
+  unsigned* ctr;
+  unsigned n;
+  int probe = 0;     // thread 0: ranges tried, from this XCD's own
+  unsigned old = 0;  // thread 0: the ticket drawn from range (xcd + probe) % 8
+  __device__ __forceinline__ int xcd() const { return (int)(blockIdx.x % kXcd); }
+  __device__ __forceinline__ unsigned lo(int c) const {
+    return (unsigned)(((unsigned long long)c * n) / kXcd);
+  }
+  __device__ __forceinline__ void draw() {
+    if (threadIdx.x == 0 && probe < kXcd) old = atomicAdd(&ctr[(xcd() + probe) % kXcd], 1u);
+  }
+  // Next item of this workgroup (uniform), or -1 when every range is exhausted.
+  __device__ __forceinline__ int next(int G4_LDS* slot) {
+    barrier_lds();  // every wave is done with the previous item's LDS
+    if (threadIdx.x == 0) {
+      int item = -1;
+      while (probe < kXcd) {
+        const int c = (xcd() + probe) % kXcd;
+        if (lo(c) + old < lo(c + 1)) {
+          item = (int)(lo(c) + old);
+          break;
+        }
+        if (++probe < kXcd) old = atomicAdd(&ctr[(xcd() + probe) % kXcd], 1u);
+      }
+      if (item < 0 && atomicAdd(&ctr[kXcd], 1u) == gridDim.x - 1u) {
+#pragma unroll
+        for (int c = 0; c <= kXcd; ++c) atomicExch(&ctr[c], 0u);
+      }
+      *slot = item;
+    }
+    barrier_lds();
+    const int t = __builtin_amdgcn_readfirstlane(*slot);
+    barrier_lds();  // every wave has read the slot before the next item's copies
+    return t;
+  }
+};
+
 // MFMA chains with A LDS operand reads in flight (kAhead unless a caller
 // picks another depth): read n + A is issued right after MFMA n and
 // sched_barrier pins that order.  Left to itself the scheduler falls back to

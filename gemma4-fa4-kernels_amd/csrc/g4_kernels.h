@@ -105,6 +105,13 @@ size_t delta_bytes(const g4_problem& p);
 size_t raise_flags_bytes(const g4_problem& p);
 size_t fwd_doc_list_bytes(const g4_problem& p);  // counter (256 B) + entries
 constexpr size_t kSchedBytes = 256;  // work-queue counters (backward workspace tail)
+// Counter words: [0] dK/dV queue, [2] dQ queue (stored dS at head dim 512,
+// recompute), [3] dQ recompute list length, [kDqXcdQueue, +9) the XcdQueue of
+// the head-dim 256 stored-dS dQ kernel; words [0, kSchedClear) are zeroed by
+// the delta pass of every backward.
+constexpr int kDqXcdQueue = 16;
+constexpr int kSchedClear = 32;
+static_assert(kSchedClear * 4 <= (int)kSchedBytes, "counters fit");
 size_t dq_list_bytes(const g4_problem& p);  // after the counters
 
 // Function attributes and occupancy are per device, and one process may drive
