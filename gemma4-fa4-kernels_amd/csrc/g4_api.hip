@@ -260,9 +260,33 @@ static size_t sums_bytes(const g4_problem& p) {
 // f(stripe) in order; returns the number of stripes (0: not striped: the dense
 // layout fits, or the problem is not a single such sequence, or not even four
 // rows reaching every key tile fit).
+// Several sequences (packed or fixed): sequence stripes instead.  Stripe k
+// takes the sequences whose first row lies in [k H, (k + 1) H), whole: their
+// rows fit H + (rows of the longest sequence) - 1 buffer rows of every key
+// tile, with H as large as the budget allows and at least the longest
+// sequence's rows (fewer would mean many nearly empty launches; such a budget
+// leaves the recompute route).  Each sequence's dK / dV come from one stripe,
+// so no sums are needed.
+template <class F>
+static int for_each_seq_stripe(const g4_problem& p, F f) {
+  const size_t cap = ds_cap(p);
+  if (cap == 0 || ds_full_bytes(p) <= cap) return 0;
+  int total_rows, ncols;
+  ds_geometry(p, &total_rows, &ncols);
+  const int64_t maxrows = (p.seqlen_q + 31) / 32;
+  const size_t per_row = (size_t)ncols * p.num_q_heads * 4096;
+  const int64_t fit = (int64_t)(cap / per_row);  // buffer rows within the budget
+  const int64_t h = fit - maxrows + 1;
+  if (h < maxrows) return 0;
+  int n = 0;
+  for (int64_t r0 = 0; r0 < total_rows; r0 += h, ++n)
+    f(DsStripe{(int)r0, (int)std::min<int64_t>(fit, total_rows - r0), ncols, (int)h});
+  return n;
+}
 template <class F>
 static int for_each_ds_stripe(const g4_problem& p, F f) {
-  if (!ds_dense_kind(p) || p.num_seqs != 1) return 0;
+  if (!ds_dense_kind(p)) return 0;
+  if (p.num_seqs > 1) return for_each_seq_stripe(p, f);
   const size_t budget = ds_cap(p);
   if (budget == 0 || ds_full_bytes(p) <= budget || budget <= sums_bytes(p)) return 0;
   const size_t cap = budget - sums_bytes(p);
@@ -288,7 +312,7 @@ static int for_each_ds_stripe(const g4_problem& p, F f) {
       if ((size_t)h2 * cols(r0 + h2) * per > cap) break;
       h = h2;
     }
-    f(DsStripe{r0, h, cols(r0 + h)});
+    f(DsStripe{r0, h, cols(r0 + h), 0});
     ++n;
     r0 += h;
   }
@@ -301,7 +325,9 @@ int ds_stripes(const g4_problem& p, DsStripe* out, int max_out) {
     ++i;
   });
 }
-size_t acc_bytes(const g4_problem& p) { return ds_stripes(p, nullptr, 0) ? sums_bytes(p) : 0; }
+size_t acc_bytes(const g4_problem& p) {
+  return p.num_seqs == 1 && ds_stripes(p, nullptr, 0) ? sums_bytes(p) : 0;
+}
 size_t ds_bytes(const g4_problem& p) {
   const bool dense = ds_dense_kind(p);
   const bool band = p.head_dim == 256 && p.window > 0;
@@ -493,8 +519,8 @@ int g4_attn_bwd(const g4_problem* p, const void* q, g4_layout ql, const void* k,
     return G4_OK;
   }
   // Striped stored dS (g4::for_each_ds_stripe): per stripe, the dK/dV launch
-  // (which stores the stripe's dS and adds to the fp32 dK / dV sums) then the
-  // dQ launch that reads them, all on the one stream.
+  // (which stores the stripe's dS; row stripes add to the fp32 dK / dV sums)
+  // then the dQ launch that reads them, all on the one stream.
   G4_TRY(check_operand(q, ql, "q"));
   G4_TRY(check_operand(k, kl, "k"));
   G4_TRY(check_operand(v, vl, "v"));
@@ -516,7 +542,9 @@ int g4_attn_bwd(const g4_problem* p, const void* q, g4_layout ql, const void* k,
   a.dkl = dkl;
   a.dvl = dvl;
   a.dk_acc = acc_ptr(*p, ws);
-  a.dv_acc = a.dk_acc + (size_t)g4::k_stream_tokens(*p) * p->num_kv_heads * p->head_dim;
+  a.dv_acc = a.dk_acc == nullptr
+                 ? nullptr
+                 : a.dk_acc + (size_t)g4::k_stream_tokens(*p) * p->num_kv_heads * p->head_dim;
   hipStream_t st = (hipStream_t)stream;
   int i = 0, rc = G4_OK;
   g4::for_each_ds_stripe(*p, [&](const g4::DsStripe& s) {
@@ -524,7 +552,8 @@ int g4_attn_bwd(const g4_problem* p, const void* q, g4_layout ql, const void* k,
     a.ds_row_lo = s.row_lo;
     a.ds_rows = s.rows;
     a.ds_cols = s.cols;
-    a.dq_qt_lo = s.row_lo / 4;
+    a.ds_seq_rows = s.seq_rows;
+    a.dq_qt_lo = s.seq_rows > 0 ? 0 : s.row_lo / 4;
     a.acc_mode = (i > 0 ? 1 : 0) | (i + 1 == nstripes ? 2 : 0);
     hipError_t e = g4::launch_bwd_dkdv(a, st);
     if (e != hipSuccess) {

@@ -112,6 +112,16 @@ struct RolesCfg {
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 };
 
+// First dS row of sequence s (see BwdParams::ds), and whether a launch of
+// sequence stripes handles the sequence (BwdParams::ds_seq_rows).
+__device__ __forceinline__ int64_t ds_first_row(const BwdParams& a, const Seq& sq, int s) {
+  return sq.packed ? sq.qtok / 32 + s : (int64_t)s * ((a.p.seqlen_q + 31) / 32);
+}
+__device__ __forceinline__ bool ds_seq_skipped(const BwdParams& a, int64_t first_row) {
+  return a.ds_seq_rows > 0 &&
+         (first_row < a.ds_row_lo || first_row >= (int64_t)a.ds_row_lo + a.ds_seq_rows);
+}
+
 // ROT: the dh = 1 P waves read the Q tile rotated by 16 rows (see step_p).
 // STRIPED: one stripe of the striped stored-dS backward (BwdParams::ds_row_lo).
 template <bool META, bool ROT, bool STRIPED>
@@ -492,7 +502,8 @@ __device__ __forceinline__ void dkdv_roles_tile(const BwdParams& a, char* smem_r
     ker.nqt = max(hi - lo, 0);
     ker.ds_row0 = -a.ds_row_lo;
   } else {
-    ker.ds_row0 = sq.packed ? sq.qtok / 32 + ker.s : (int64_t)ker.s * ((p.seqlen_q + 31) / 32);
+    // (sequence stripes: rows from the stripe's first, ds_row_lo; else 0)
+    ker.ds_row0 = ds_first_row(a, sq, ker.s) - a.ds_row_lo;
   }
   const int nsteps = ker.nqt * ker.grp;
   ker.ds_lane = (ker.kb * 32 + (ker.lane & 31)) * 64 + 32 * ker.dh + 8 * ker.h32;
@@ -561,7 +572,7 @@ __device__ __forceinline__ void dkdv_roles_pair(const BwdParams& a, char* smem_r
   }
   const Seq sq = resolve_seq(a.p, s);
   const int nt = (sq.lk + C::kBN - 1) / C::kBN;
-  if (r >= (nt + 1) / 2) return;
+  if (r >= (nt + 1) / 2 || ds_seq_skipped(a, ds_first_row(a, sq, s))) return;
 #pragma nounroll
   for (int pass = 0; pass < 2; ++pass) {
     const int kt = pass == 0 ? r : nt - 1 - r;
@@ -588,8 +599,11 @@ __global__ void __launch_bounds__(RolesCfg::kNT, 1) dkdv_roles_kernel(BwdParams 
     if (by_length) {
       // ordered by query length; units: pairs of key tiles over all KV heads
       SeqUnitsByLength order;
-      order.init(a.p.cu_seqlens_q, a.p.cu_seqlens_k, a.num_seqs,
-                 [&](int lk) { return ((lk + C::kBN - 1) / C::kBN + 1) / 2 * hkv; });
+      // (sequence stripes: only the stripe's sequences)
+      order.init(a.p.cu_seqlens_q, a.p.cu_seqlens_k, a.num_seqs, [&](int seq, int lk) {
+        const int64_t first_row = a.p.cu_seqlens_q[seq] / 32 + seq;
+        return ds_seq_skipped(a, first_row) ? 0 : ((lk + C::kBN - 1) / C::kBN + 1) / 2 * hkv;
+      });
       n = order.total;
       if (threadIdx.x < 64) order.store((int G4_LDS*)(smem_raw + C::kLdsSeq));
       barrier_lds();
@@ -1825,11 +1839,11 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
 
   ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
   ker.kstride = a.kl.token_stride;
-  // (striped: the stripe's rows of the one sequence, from the buffer's first)
-  const int64_t row0 =
-      (a.dk_acc != nullptr ? -(int64_t)a.ds_row_lo
-                           : sq.packed ? sq.qtok / 32 + s : (int64_t)s * ((p.seqlen_q + 31) / 32)) +
-      i0 / 32;
+  // (row stripes: the one sequence's rows; sequence stripes: rows from the
+  // stripe's first, ds_row_lo, and only the stripe's sequences)
+  const int64_t first_row = ds_first_row(a, sq, s);
+  if (ds_seq_skipped(a, first_row)) return;
+  const int64_t row0 = (a.dk_acc != nullptr ? 0 : first_row) + i0 / 32 - a.ds_row_lo;
   ker.ds_head_stride = (int64_t)a.ds_rows * a.ds_cols * 4096;
   if constexpr (kBand) {
     ker.ds_col_stride = 4096;

@@ -540,7 +540,8 @@ struct SeqTiles {
 // in that order.
 struct SeqUnitsByLength {
   int cnt, lo, total;
-  // cu_len orders the sequences; units(length from cu_cnt) counts their units.
+  // cu_len orders the sequences; units(sequence, length from cu_cnt) counts
+  // their units.
   template <class Units>
   __device__ __forceinline__ void init(const int* cu_len, const int* cu_cnt, int nseq,
                                        Units units) {
@@ -549,7 +550,7 @@ struct SeqUnitsByLength {
     cnt = 0;
     if (lane < nseq) {
       len = cu_len[lane + 1] - cu_len[lane];
-      cnt = units(cu_cnt[lane + 1] - cu_cnt[lane]);
+      cnt = units(lane, cu_cnt[lane + 1] - cu_cnt[lane]);
     }
     int before = 0;
     for (int j = 0; j < nseq; ++j) {

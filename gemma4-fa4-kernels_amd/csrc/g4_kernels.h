@@ -74,11 +74,14 @@ struct BwdParams {
   // order, so each lane stores one 32-byte run).
   __bf16* ds;
   int ds_rows, ds_cols;
-  // Striped stored-dS backward (head dim 512, one causal sequence whose dense
-  // dS exceeds the budget; see DsStripe): the buffer holds rows
-  // [ds_row_lo, ds_row_lo + ds_rows) of this launch's stripe, and the dQ
-  // launch takes the stripe's 128-query tiles from dq_qt_lo.  0 otherwise.
-  int ds_row_lo, dq_qt_lo;
+  // Striped stored-dS backward (head dim 512, dense dS past the budget; see
+  // DsStripe).  Row stripes (one sequence, dk_acc set): the buffer holds the
+  // sequence's rows [ds_row_lo, ds_row_lo + ds_rows), and the dQ launch takes
+  // the stripe's 128-query tiles from dq_qt_lo.  Sequence stripes
+  // (ds_seq_rows > 0): the launch handles only the sequences whose first row
+  // lies in [ds_row_lo, ds_row_lo + ds_seq_rows), whole, and the buffer holds
+  // rows from ds_row_lo.  All 0 otherwise.
+  int ds_row_lo, dq_qt_lo, ds_seq_rows;
   // fp32 dK / dV sums over the stripes ((Tk, Hkv, D), null unless striped) and
   // what the dK/dV launch's epilogue does with them: bit 0 adds the stored
   // sums (every stripe after the first), bit 1 writes the bf16 dK / dV (the
@@ -170,17 +173,20 @@ struct PersistentGrid {
 // dS buffer of the head-dim 512 causal backward (0: the dQ stage recomputes S, dP).
 size_t ds_bytes(const g4_problem& p);
 void ds_geometry(const g4_problem& p, int* rows, int* cols);
-// A stripe of the striped stored-dS backward: 32-query rows [row_lo, row_lo +
-// rows) (rows a multiple of 4, so stripes hold whole 128-query dQ tiles) and the
-// key tiles they reach (cols).
+// A stripe of the striped stored-dS backward, buffer geometry rows x cols.
+// Row stripe (seq_rows = 0, one sequence): its 32-query rows [row_lo, row_lo +
+// rows) (a multiple of 4, so stripes hold whole 128-query dQ tiles) and the
+// key tiles they reach (cols).  Sequence stripe (seq_rows > 0, several
+// sequences): the sequences whose first row lies in [row_lo, row_lo +
+// seq_rows), whose rows all fit in the buffer's rows from row_lo.
 struct DsStripe {
-  int row_lo, rows, cols;
+  int row_lo, rows, cols, seq_rows;
 };
-// Stripes of a problem whose dense dS exceeds its budget: one causal head-dim
-// 512 sequence whose rows fit in stripes of at least four rows; writes up to
+// Stripes of a causal head-dim 512 problem whose dense dS exceeds its budget:
+// row stripes of one sequence, sequence stripes of several; writes up to
 // max_out of them and returns how many there are (0: not striped).
 int ds_stripes(const g4_problem& p, DsStripe* out, int max_out);
-// fp32 dK / dV sums of the striped backward (0 when not striped).
+// fp32 dK / dV sums of the row-striped backward (0 otherwise).
 size_t acc_bytes(const g4_problem& p);
 int64_t k_stream_tokens(const g4_problem& p);
 int64_t q_stream_tokens(const g4_problem& p);

@@ -75,8 +75,8 @@ typedef struct g4_problem {
   /* Bytes of the backward workspace that may hold dS tiles stored by the
    * dK/dV stage for the dQ stage: 0 = the library default (16 GiB), < 0 =
    * none.  When the tiles a problem needs exceed the budget, g4_attn_bwd
-   * stripes a single head-dim 512 causal sequence (see g4_attn_bwd); in every
-   * other case none are stored and the dQ stage recomputes S and dP (slower,
+   * stripes head-dim 512 causal problems (see g4_attn_bwd); in every other
+   * case none are stored and the dQ stage recomputes S and dP (slower,
    * workspace O(T) instead of O(T * Sk)).  Results are the same on every
    * route up to fp32 summation order.
    * The reference's global backward budget policy is the analogous knob
@@ -148,14 +148,20 @@ int g4_attn_fwd_static(const g4_problem* p,
  * Backward: dQ, dK, dV given O, dO, LSE and optional dLSE (same layout as LSE,
  * NULL = zero).  dK and dV are distinct outputs; no atomics (bitwise
  * repeatable).  Runs g4_attn_bwd_delta, g4_attn_bwd_dkdv and g4_attn_bwd_dq.
- * Striped route: a problem of one head-dim 512 causal sequence whose dense dS
- * tiles exceed ds_budget is cut into stripes of 32-query rows, each stripe's
- * tiles fitting the budget beside fp32 dK / dV sums (2 x K tokens x KV heads
- * x 512 x 4 bytes, counted in the budget and in g4_workspace_bytes); the
- * dK/dV and dQ launches then alternate per stripe, so nothing is recomputed.
- * dQ is then bitwise that of the dense stored route; dK and dV differ from it
- * by the fp32 additions between stripes.  (The three stage entry points on
- * such a problem take the recompute route instead.)
+ * Striped routes, for head-dim 512 causal problems whose dense dS tiles
+ * exceed ds_budget; the dK/dV and dQ launches alternate per stripe, so
+ * nothing is recomputed:
+ *   - one sequence: stripes of 32-query rows, each stripe's tiles fitting the
+ *     budget beside fp32 dK / dV sums (2 x K tokens x KV heads x 512 x 4
+ *     bytes, counted in the budget and in g4_workspace_bytes).  dQ is bitwise
+ *     that of the dense stored route; dK and dV differ from it by the fp32
+ *     additions between stripes.
+ *   - several sequences: stripes of whole sequences (those whose first dS row
+ *     falls in the stripe), when the budget holds at least two longest
+ *     sequences' rows of tiles.  dQ, dK and dV are bitwise those of the dense
+ *     stored route.
+ * (The three stage entry points on such a problem take the recompute route
+ * instead.)
  * Replaces FA4's autograd backward (local) and the patched global d512
  * orchestrator _flash_attn_bwd_gemma4_global_d512
  * (patches/flash-attention/0002-*.patch:1021-1512, called from

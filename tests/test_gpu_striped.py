@@ -216,3 +216,112 @@ def test_global_sequence_past_the_default_ds_budget():
     assert torch.equal(routes["recompute"][4], routes["dense"][4])
     for i in (3, 4):
         assert _rel(routes["striped"][i], routes["dense"][i]) < 2e-3
+
+
+# ---------------------------------------------------------------------------
+# Sequence stripes: several sequences (packed or fixed) past the budget.
+# ---------------------------------------------------------------------------
+
+
+def _run_multi(q, k, v, do, dlse, lq, lk, *, docs=None, ds_budget=0, packed=True):
+    """g4_attn_fwd + g4_attn_bwd on a packed (T, H, D) or fixed (B, S, H, D) batch."""
+    from gemma4_fa4_amd import ops
+
+    cq, ck = cu(lq), cu(lk)
+    plan = ops.make_plan(
+        num_seqs=len(lq), seqlen_q=max(lq), seqlen_k=max(lk), num_q_heads=q.shape[1],
+        num_kv_heads=k.shape[1], head_dim=512, window=None,
+        documents=None if docs is None else docs.to(DEV),
+        cu_q=cq.to(DEV) if packed else None, cu_k=ck.to(DEV) if packed else None,
+        total_q=q.shape[0], total_k=k.shape[0], ds_budget=ds_budget)
+    if not packed:  # B equal sequences: (B, S, H, D) views of the packed buffers
+        b = len(lq)
+        q, k, v, do = (t.view(b, t.shape[0] // b, *t.shape[1:]) for t in (q, k, v, do))
+        dlse = dlse.view(dlse.shape[0], b, -1).permute(1, 0, 2).contiguous()
+    st = ops.Stages(plan, q.to(DEV), k.to(DEV), v.to(DEV), do.to(DEV), dlse.to(DEV))
+    st.forward()
+    st.backward()
+    torch.cuda.synchronize()
+    flat = (lambda t: t) if packed else (lambda t: t.reshape(-1, *t.shape[2:]))
+    return [flat(t).cpu() for t in (st.dq, st.dk, st.dv)], plan
+
+
+def _seq_budget(lq, lk, hq, packed, extra):
+    """Budget (bytes) whose stripes hold H = longest rows + extra first rows each."""
+    rows_max = (max(lq) + 31) // 32
+    per_row = (max(lk) + 63) // 64 * hq * 4096
+    dense_rows = sum(lq) // 32 + len(lq) if packed else len(lq) * rows_max
+    fit = 2 * rows_max - 1 + extra
+    assert fit < dense_rows, "the batch must not fit the budget"
+    return fit * per_row, dense_rows * per_row
+
+
+SEQ_CASES = [
+    # (lq, lk, hq, hkv, packed, docs, extra rows)
+    ([300, 0, 517, 96, 1000, 64, 700], [300, 40, 600, 96, 1000, 64, 700], 8, 1, True, False, 0),
+    ([1024] * 3, [1024] * 3, 16, 2, False, False, 7),  # fixed layout, an empty last stripe
+    ([800, 1200, 30, 900], [900, 1200, 30, 1000], 8, 2, True, True, 5),  # documents
+    ([400] * 70, [400] * 70, 8, 8, True, False, 3),  # > 64 sequences, work-queue launch
+    ([1024] * 40, [1024] * 40, 8, 4, True, False, 20),  # by-length work-queue launch
+]
+
+
+@pytest.mark.parametrize("lq,lk,hq,hkv,packed,with_docs,extra", SEQ_CASES)
+def test_sequence_stripes_match_the_dense_route(lq, lk, hq, hkv, packed, with_docs, extra):
+    # Each sequence is handled whole by one stripe's launches of the same
+    # kernels: dQ, dK and dV equal the dense stored-dS route's to the bit.
+    label = f"sequence stripes n={len(lq)} hq={hq} hkv={hkv} packed={packed} docs={with_docs}"
+    print(label, flush=True)
+    q, k, v, do, dlse = qkv(9800 + len(lq) + hkv, sum(lq), sum(lk), hq, hkv, 512)
+    docs = None
+    if with_docs:
+        docs = torch.zeros(sum(lk), dtype=torch.int32)
+        docs[500:] = 1
+        docs[1700:] = 2
+    budget, dense_bytes = _seq_budget(lq, lk, hq, packed, extra)
+    got, plan = _run_multi(q, k, v, do, dlse, lq, lk, docs=docs, ds_budget=budget,
+                           packed=packed)
+    assert 0 < _stored_bytes(plan) <= budget, "the batch is not striped"
+    dense, dplan = _run_multi(q, k, v, do, dlse, lq, lk, docs=docs, packed=packed)
+    assert _stored_bytes(dplan) == dense_bytes
+    for i, name in enumerate(("dQ", "dK", "dV")):
+        assert torch.equal(got[i], dense[i]), f"{name} differs from the dense route"
+    if len(lq) <= 8:
+        cq, ck = cu(lq), cu(lk)
+        args = dict(document_ids=None if docs is None else docs.to(DEV))
+        _o, _l, *refs = attention_fwd_bwd(
+            q.to(DEV), k.to(DEV), v.to(DEV), cq.tolist(), ck.tolist(), do=do.to(DEV),
+            dlse=dlse.to(DEV), compute_dtype=torch.float64, **args)
+        _, bq, bk, bv = bf16_baseline_fwd_bwd(q.to(DEV), k.to(DEV), v.to(DEV), cq.tolist(),
+                                              ck.tolist(), do=do.to(DEV), dlse=dlse.to(DEV),
+                                              **args)
+        check_gradients(got, [t.cpu() for t in refs], [t.cpu() for t in (bq, bk, bv)],
+                        label=label)
+
+
+def test_packed_adapter_backward_takes_sequence_stripes():
+    # Through fa4_global_varlen_forward: a pinned budget below the batch's dense
+    # tiles but above two longest sequences' rows gives the striped route, with
+    # gradients equal to the dense route's.
+    import gemma4_fa4_amd as g
+
+    lq = [700, 1500, 300, 1100]
+    q, k, v, do, _dl = qkv(9850, sum(lq), sum(lq), 32, 4, 512)
+    q, k, v, do = (t.to(DEV) for t in (q, k, v, do))
+    c = cu(lq).to(DEV)
+    budget, _dense = _seq_budget(lq, lq, 32, True, 2)
+    grads = {}
+    for name, pin in (("striped", budget), ("dense", 1 << 34)):
+        print(f"packed adapter backward: {name}", flush=True)
+        previous = g.pin_backward_ds_budget(pin)
+        try:
+            qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
+            o, _lse = g.fa4_global_varlen_forward(qd, kd, vd, c, c, max_seqlen_q=max(lq),
+                                                  max_seqlen_k=max(lq))
+            torch.autograd.backward(o, do)
+            torch.cuda.synchronize()
+        finally:
+            g.pin_backward_ds_budget(previous)
+        grads[name] = [t.grad.cpu() for t in (qd, kd, vd)]
+    for a, b in zip(grads["striped"], grads["dense"]):
+        assert torch.equal(a, b)

@@ -121,6 +121,38 @@ def test_ds_budget_sizes_the_stored_dS_tiles():
     assert lib.g4_workspace_bytes(ctypes.byref(p2), 1) == lean
 
 
+def test_ds_budget_sequence_stripes_of_several_sequences():
+    # Several d512 causal sequences past the budget are striped by sequence:
+    # stripe k takes the sequences whose first dS row lies in [k H, (k + 1) H)
+    # and needs H + 63 buffer rows (the longest sequence, 2048 queries, has 64
+    # rows), with H as large as fits and at least 64; no fp32 sums.
+    import ctypes
+    lib = _lib.load()
+    cu = (ctypes.c_int32 * 5)(0, 1000, 3048, 3100, 4096)  # never read on the host
+    per_row = 32 * 32 * 4096  # 32 key tiles x 32 heads x 4 KB
+
+    def ws(budget, packed=True):
+        p = _lib.G4Problem(num_seqs=4, seqlen_q=2048, seqlen_k=2048, num_q_heads=32,
+                           num_kv_heads=4, head_dim=512, window=0, total_q=4096,
+                           total_k=4096, ds_budget=budget)
+        if packed:
+            p.cu_seqlens_q = p.cu_seqlens_k = ctypes.cast(cu, ctypes.c_void_p)
+        return lib.g4_workspace_bytes(ctypes.byref(p), 1)
+
+    lean = ws(-1)
+    assert ws(0) - lean == (4096 // 32 + 4) * per_row  # dense: 132 packed rows fit 16 GiB
+    assert ws(132 * per_row) - lean == 132 * per_row
+    # 127 rows: H = 127 - 63 = 64, stripes from rows 0, 64, 128 (127, 68 and 4 rows)
+    assert ws(127 * per_row) - lean == 127 * per_row
+    assert ws(131 * per_row) - lean == 131 * per_row  # H = 68: stripes of 131 and 64 rows
+    # 126 rows: H = 63 < 64, recompute
+    assert ws(127 * per_row - 1) == lean
+    # fixed layout, 4 x 2048: 256 rows; 200 rows give H = 137 (stripes of 200, 119)
+    flean = ws(-1, packed=False)
+    assert ws(200 * per_row, packed=False) - flean == 200 * per_row
+    assert ws(0, packed=False) - flean == 256 * per_row
+
+
 @pytest.mark.parametrize("make,ok", [
     (lambda: torch.zeros(1, 64, 32, 256, dtype=torch.bfloat16), True),
     (lambda: torch.zeros(256, dtype=torch.bfloat16).expand(1, 64, 32, 256), False),
