@@ -1,4 +1,4 @@
-"""C-ABI parity of the striped stored-dS backward (head dim 512, one causal sequence).
+"""C-ABI parity of the striped stored-dS backward (head dim 512, causal).
 
 When the dense dS tiles of a single global sequence exceed the problem's
 ``ds_budget``, ``g4_attn_bwd`` cuts its 32-query rows into stripes that fit the
@@ -11,6 +11,8 @@ route's only by the fp32 additions between stripes.  Each case is checked
 against the dense route and against the fp64 oracle with the reference's M1
 envelopes: several stripes (ragged last stripe, keys before the first query,
 documents, the work-queue launch) and the smallest budget that still stripes.
+Several sequences past the budget are striped by whole sequences instead (no
+sums), and their gradients must equal the dense route's to the bit.
 """
 
 import pytest
