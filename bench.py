@@ -21,7 +21,8 @@ fp32 CPU oracle timed on this host (configuration 1 in full, forward-only and
 forward+backward of a bounded head sample of configuration 2).
 
 Also reported: the long-context row (configuration 6: one 65536-token global
-sequence, the reference's S64K row, 3 timed steps after 1 warm-up), and a
+sequence, the reference's S64K row, 3 timed steps after 1 warm-up), one-token
+decode latency against 8K and 128K global caches and an 8K local cache, and a
 measured bf16 GEMM rate (torch.matmul on 8192^3 random bf16 operands) as a
 second denominator beside the 2.5 PFLOP/s dense peak, as the reference divides
 by its measured GEMM rate (experiments/EXP-0029-h100-performance-baseline.md:70-71).
@@ -315,6 +316,32 @@ def kv_prep_timing(torch, dev, reps: int):
     return out
 
 
+def decode_timing(torch, dev, reps: int):
+    """One-token decode (Sq = 1, lower-right, B = 1) through g4_attn_fwd: the
+    split-key forward.  K/V bytes are the cache the step must read (the window
+    for the local layer); GB/s is those bytes over the median call."""
+    from gemma4_fa4_amd import ops
+
+    out = {}
+    for d, hq, hkv, window, sk in ((512, 32, 4, None, 8192), (512, 32, 4, None, 131072),
+                                   (256, 32, 16, 1024, 8192)):
+        g = torch.Generator(device=dev).manual_seed(sk)
+        q = torch.randn(1, 1, hq, d, generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn(1, sk, hkv, d, generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn(1, sk, hkv, d, generator=g, device=dev).to(torch.bfloat16)
+        plan = ops.make_plan(num_seqs=1, seqlen_q=1, seqlen_k=sk, num_q_heads=hq,
+                             num_kv_heads=hkv, head_dim=d, window=window)
+        st = ops.Stages(plan, q, k, v, q, forward_only=True)
+        ms = statistics.median(event_times(torch, st.forward, reps, 2))
+        keys = sk if window is None else min(sk, window)
+        kv_bytes = 2 * keys * hkv * d * 2
+        label = f"{'global' if window is None else 'local'}_d{d}_Sk{sk}"
+        out[label] = {"us": round(ms * 1e3, 1), "kv_bytes": kv_bytes,
+                      "gbs": round(kv_bytes / (ms * 1e-3) / 1e9, 1)}
+        del st, q, k, v
+    return out
+
+
 def gemm_rate(torch, dev, reps: int = 10, n: int = 8192) -> float:
     """Measured bf16 GEMM rate (TFLOP/s): torch.matmul of random n x n operands.
 
@@ -490,6 +517,7 @@ def main() -> int:
                 torch, g, w, steps=min(args.steps, 3) if long_ctx else args.steps,
                 warmup=1 if long_ctx else args.warmup, dev=dev)
             torch.cuda.empty_cache()
+        extra["decode_one_token"] = decode_timing(torch, dev, max(10, args.steps))
         gemm = gemm_rate(torch, dev)
         extra["measured_bf16_gemm_tflops"] = round(gemm, 1)
         extra["config2_fwd_bwd_pct_of_measured_gemm"] = round(100.0 * head["fwd_bwd_tflops"] / gemm, 2)

@@ -90,10 +90,11 @@ int check_ws(const g4_problem* p, int phase, void* ws, size_t bytes) {
     if (_rc != G4_OK) return _rc; \
   } while (0)
 
-// Workspace: [spans][raise flags][document-pass list] (forward); backward adds
+// Workspace: [spans][raise flags][document-pass list][split partials] (forward); backward adds
 // [delta][dS][queue counters][dQ recompute list][dK / dV sums (striped)]
 size_t fwd_ws_bytes(const g4_problem& p) {
-  return align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) + g4::fwd_doc_list_bytes(p);
+  return align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) + g4::fwd_doc_list_bytes(p) +
+         g4::split_bytes(p);
 }
 int* raise_flags_ptr(const g4_problem& p, void* ws) {
   return g4::raise_flags_bytes(p) ? (int*)((char*)ws + align256(g4::spans_bytes(p))) : nullptr;
@@ -101,6 +102,11 @@ int* raise_flags_ptr(const g4_problem& p, void* ws) {
 unsigned* fwd_doc_list_ptr(const g4_problem& p, void* ws) {
   if (!g4::fwd_doc_list_bytes(p)) return nullptr;
   return (unsigned*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p));
+}
+float* split_ptr(const g4_problem& p, void* ws) {
+  if (!g4::split_bytes(p)) return nullptr;
+  return (float*)((char*)ws + align256(g4::spans_bytes(p)) + g4::raise_flags_bytes(p) +
+                  g4::fwd_doc_list_bytes(p));
 }
 float* delta_ptr(const g4_problem& p, void* ws) {
   return (float*)((char*)ws + fwd_ws_bytes(p));
@@ -179,6 +185,8 @@ int fwd_impl(const g4_problem* p, const void* q, g4_layout ql, const void* k, g4
   }
   g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);
   a.raise_flags = raise_flags_ptr(*p, ws);
+  a.part = split_ptr(*p, ws);
+  if (a.part != nullptr) a.split_chunks = g4::split_chunks(*p, &a.split_keys);
   if (unsigned* dl = fwd_doc_list_ptr(*p, ws)) {
     a.doc_list_n = dl;
     a.doc_list = (int*)(dl + 64);
@@ -360,6 +368,37 @@ size_t fwd_doc_list_bytes(const g4_problem& p) {
 size_t raise_flags_bytes(const g4_problem& p) {
   if (p.head_dim != 512) return 0;
   return align256((size_t)p.num_seqs * ((p.seqlen_q + 31) / 32) * p.num_q_heads * 4);
+}
+// Split-key forward: problems without key metadata whose query rows of one KV
+// head (query heads of the group x queries) fit one 32-row tile, over at least
+// 256 keys: one workgroup per (sequence, KV head, chunk of keys) instead of one
+// per (query tile, query head), each walking every key (a decode step of one
+// query then reads the K/V cache eight times over, in 32 workgroups).  About
+// two rounds of resident workgroups in all (head dim 512: one per CU, 256:
+// two), each chunk a whole number of 32-key tiles, at least four (head dim
+// 512) or two.
+int split_chunks(const g4_problem& p, int* keys) {
+  if ((p.vision_ids != nullptr && p.bidirectional_vision) || p.document_ids != nullptr) return 0;
+  const int64_t rows = (int64_t)(p.num_q_heads / p.num_kv_heads) * p.seqlen_q;
+  if (rows > 32) return 0;
+  const int64_t range = p.window > 0 ? std::min<int64_t>(p.seqlen_k, (int64_t)p.window + p.seqlen_q)
+                                     : p.seqlen_k;
+  if (range < 256) return 0;
+  const int64_t target = p.head_dim == 512 ? 512 : 1024;
+  const int64_t min_tiles = p.head_dim == 512 ? 4 : 2;
+  const int64_t groups = (int64_t)p.num_seqs * p.num_kv_heads;
+  const int64_t tiles = (range + 31) / 32 + 1;  // (the range may start mid-tile)
+  int64_t n = std::max<int64_t>(1, std::min((target + groups - 1) / groups, tiles / min_tiles));
+  const int64_t per = (tiles + n - 1) / n;  // tiles per chunk
+  n = (tiles + per - 1) / per;
+  if (keys != nullptr) *keys = (int)(per * 32);
+  return (int)n;
+}
+size_t split_bytes(const g4_problem& p) {
+  const int n = split_chunks(p, nullptr);
+  if (n == 0) return 0;
+  const size_t rows = (size_t)(p.num_q_heads / p.num_kv_heads) * p.seqlen_q;
+  return align256((size_t)p.num_seqs * p.num_kv_heads * n * rows * (p.head_dim + 2) * 4);
 }
 }  // namespace g4
 

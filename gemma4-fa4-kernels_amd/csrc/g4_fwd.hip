@@ -526,6 +526,185 @@ __global__ void __launch_bounds__(NQG * DSPLIT * 64, OCC) fwd_kernel(FwdParams a
 }
 
 // ===========================================================================
+// Split-key forward for few queries per KV head (decode).
+//
+// One workgroup per (sequence, KV head, chunk of split_keys keys): its 32
+// rows are the query rows of the KV head's group, row r = query head
+// kvh * grp + r / Sq, query r % Sq (grp * Sq <= 32; the rest are zero rows),
+// so each K / V tile is read once for the whole group, and the chunks spread a
+// long key range over the GPU.  The steps are FwdKernel's (one 32-row group,
+// head dim split over D / 256 waves); the workgroup writes its rows' partial
+// state (O not normalised, running maximum m in log2 units, row sum l) and
+// merge_split_kernel combines the chunks: with M the largest m,
+// O = sum 2^(m_c - M) O_c / sum 2^(m_c - M) l_c.
+// ===========================================================================
+
+template <int D>
+using SplitKernel = FwdKernel<D, 32, D / 256, 1, true, 0, (D == 256 ? 2 : 1)>;
+
+template <int D>
+__global__ void __launch_bounds__(D / 4, (D == 256 ? 2 : 1)) fwd_split_kernel(FwdParams a) {
+  using K = SplitKernel<D>;
+  using C = typename K::C;
+  constexpr int BN = 32;
+  extern __shared__ __attribute__((aligned(16))) char smem_raw[];
+  K ker;
+  ker.smem = (char G4_LDS*)smem_raw;
+  ker.p = &a.p;
+  const g4_problem& p = a.p;
+  ker.tid = threadIdx.x;
+  ker.lane = ker.tid & 63;
+  ker.wave = __builtin_amdgcn_readfirstlane(ker.tid >> 6);
+  ker.dh = ker.wave;
+  ker.h32 = ker.lane >> 5;
+  const int r = ker.lane & 31;
+
+  // ---- item: (sequence, KV head) group g, chunk c ---------------------------
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int n = a.split_chunks;
+  const int g = L / n, c = L % n;
+  const int s = g / p.num_kv_heads, kvh = g % p.num_kv_heads;
+  const int grp = p.num_q_heads / p.num_kv_heads;
+  const int rows = grp * p.seqlen_q;  // row stride of the partial buffers
+  ker.sq = resolve_seq(p, s);
+  const Seq& sq = ker.sq;
+  const int lq = sq.lq;
+  if (lq <= 0) return;
+  const int off = sq.lk - lq;
+  const bool valid = r < grp * lq;
+  const int qh = kvh * grp + (valid ? r / lq : 0);
+  const int qi = valid ? r % lq : 0;
+  ker.my_a = qi + off;
+  ker.a0 = off;  // the first query's position (the full-tile test's lower bound)
+  ker.has_vid = ker.has_doc = ker.has_meta = false;
+  ker.my_vid = -1;
+  ker.my_doc = 0;
+
+  // ---- this chunk's key tiles ------------------------------------------------
+  int klo, khi;
+  query_tile_key_range(off, off + lq - 1, sq.lk, p.window, -1, klo, khi);
+  const int per = a.split_keys / BN;
+  const int t_first = klo / BN + c * per;
+  const int t_end = min((khi + BN - 1) / BN, t_first + per);
+  const int ntiles = khi > klo ? max(t_end - t_first, 0) : 0;
+
+  ker.kbase = a.k + tok_off(sq, s, sq.ktok, 0, a.kl) + (int64_t)kvh * a.kl.head_stride;
+  ker.vbase = a.v + tok_off(sq, s, sq.ktok, 0, a.vl) + (int64_t)kvh * a.vl.head_stride;
+  ker.kstride = a.kl.token_stride;
+  ker.vstride = a.vl.token_stride;
+  ker.krd.init(ker.lane, ker.dh * C::kDH * 2);
+  ker.vrd.init(ker.lane, ker.dh * C::kDH * 2);
+  ker.kcp.init(ker.kstride, ker.wave, ker.lane);
+  ker.vcp.init(ker.vstride, ker.wave, ker.lane);
+  {
+    const __bf16* qrow = a.q + tok_off(sq, s, sq.qtok, qi, a.ql) +
+                         (int64_t)qh * a.ql.head_stride + ker.dh * C::kDH + ker.h32 * 8;
+#pragma unroll
+    for (int cc = 0; cc < K::kNC; ++cc) {
+      bf16x8 x = ld_global16(qrow + cc * 16);
+      ker.qf[cc] = valid ? x : bf16x8{};
+    }
+  }
+  if (ntiles > 0) {
+    ker.issue_k(t_first * BN, 0);
+    ker.issue_v(t_first * BN, 0);
+  }
+#pragma unroll
+  for (int b = 0; b < K::kNB; ++b) ker.o_acc[b] = f32x16{};
+  ker.m_run = kNegInf;
+  ker.l_run = 0.f;
+  for (int it = 0; it < ntiles; ++it) ker.step(it & 1, it, ntiles, t_first);
+
+  // ---- partial rows ---------------------------------------------------------
+  const float l_tot = ker.l_run + wave_xor32(ker.l_run);
+  if (valid) {
+    const int64_t row = ((int64_t)g * n + c) * rows + r;
+    float* po = a.part + row * D;
+#pragma unroll
+    for (int b = 0; b < K::kNB; ++b)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = ker.dh * C::kDH + b * 32 + 8 * r4 + 4 * ker.h32;
+        const f32x16& x = ker.o_acc[b];
+        *(f32x4*)(po + d) = f32x4{x[r4 * 4], x[r4 * 4 + 1], x[r4 * 4 + 2], x[r4 * 4 + 3]};
+      }
+    if (ker.dh == 0 && ker.h32 == 0) {
+      float* ml = a.part + (int64_t)p.num_seqs * p.num_kv_heads * n * rows * D + row * 2;
+      ml[0] = ker.m_run;
+      ml[1] = l_tot;
+    }
+  }
+}
+
+// One 64-lane workgroup per (sequence, KV head, row): the chunks in order.
+template <int D>
+__global__ void __launch_bounds__(64) merge_split_kernel(FwdParams a) {
+  constexpr int E = D / 64;  // elements per lane: 4 (D = 256) or 8 (D = 512)
+  const g4_problem& p = a.p;
+  const int grp = p.num_q_heads / p.num_kv_heads;
+  const int rows = grp * p.seqlen_q;
+  const int n = a.split_chunks;
+  const int g = blockIdx.x / rows, r = blockIdx.x % rows;
+  const int s = g / p.num_kv_heads, kvh = g % p.num_kv_heads;
+  const Seq sq = resolve_seq(p, s);
+  if (r >= grp * sq.lq) return;
+  const int qh = kvh * grp + r / sq.lq, qi = r % sq.lq;
+  const int lane = threadIdx.x;
+  const float* ml = a.part + (int64_t)p.num_seqs * p.num_kv_heads * n * rows * D;
+  const int64_t row0 = (int64_t)g * n * rows + r;  // chunk c: row0 + c * rows
+  float mx = kNegInf;
+  for (int c = 0; c < n; ++c) {
+    const float* e = ml + (row0 + (int64_t)c * rows) * 2;
+    if (e[1] > 0.f) mx = fmaxf(mx, e[0]);
+  }
+  float acc[E] = {};
+  float l = 0.f;
+  for (int c = 0; c < n; ++c) {
+    const int64_t row = row0 + (int64_t)c * rows;
+    const float* e = ml + row * 2;
+    if (!(e[1] > 0.f)) continue;
+    const float w = fast_exp2(e[0] - mx);
+    l += w * e[1];
+    const float* po = a.part + row * D;
+#pragma unroll
+    for (int h = 0; h < E / 4; ++h) {
+      const f32x4 x = *(const f32x4*)(po + h * 256 + 4 * lane);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[4 * h + u] += w * x[u];
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  __bf16* orow = a.o + tok_off(sq, s, sq.qtok, qi, a.ol) + (int64_t)qh * a.ol.head_stride;
+#pragma unroll
+  for (int h = 0; h < E / 4; ++h)
+    *(bf16x4*)(orow + h * 256 + 4 * lane) =
+        bf16x4{(__bf16)(acc[4 * h] * inv), (__bf16)(acc[4 * h + 1] * inv),
+               (__bf16)(acc[4 * h + 2] * inv), (__bf16)(acc[4 * h + 3] * inv)};
+  if (lane == 0)
+    a.lse[lse_off(p, sq, s, qh, qi)] = l > 0.f ? (mx + fast_log2(l)) * kLn2 : kNegInf;
+}
+
+template <int D>
+static hipError_t launch_fwd_split(const FwdParams& a, hipStream_t stream) {
+  using C = typename SplitKernel<D>::C;
+  static_assert(C::kNT == D / 4, "one wave per 256 of the head dim");
+  static LdsAttr attr;
+  hipError_t e = attr.ensure((const void*)fwd_split_kernel<D>, C::kLdsBytes);
+  if (e != hipSuccess) return e;
+  const int64_t groups = (int64_t)a.num_seqs * a.p.num_kv_heads;
+  const int64_t rows = (int64_t)(a.p.num_q_heads / a.p.num_kv_heads) * a.p.seqlen_q;
+  const int64_t items = groups * a.split_chunks;
+  if (items <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fwd_split_kernel<D>, dim3((unsigned)items), dim3(C::kNT), C::kLdsBytes,
+                     stream, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(merge_split_kernel<D>, dim3((unsigned)(groups * rows)), dim3(64), 0, stream,
+                     a);
+  return hipGetLastError();
+}
+
+// ===========================================================================
 // Software-pipelined forward for wide heads without key metadata.
 //
 // Four waves, one per SIMD, each owning 32 queries and the whole head dim, so
@@ -834,6 +1013,11 @@ __global__ void clear_list_kernel(unsigned* n) {
 }
 
 hipError_t launch_fwd(const FwdParams& a, hipStream_t stream) {
+  if (a.split_chunks > 0) {
+    if (a.p.head_dim == 256) return launch_fwd_split<256>(a, stream);
+    if (a.p.head_dim == 512) return launch_fwd_split<512>(a, stream);
+    return hipErrorInvalidValue;
+  }
   if (a.p.head_dim == 256) {
     // Two workgroups of 32-key tiles share a CU (the register file holds two
     // waves per SIMD).  With both vision and document IDs the mask state needs

@@ -36,6 +36,12 @@ struct FwdParams {
   // Full grid whose XCD runs hold whole rank pairs (set by the launcher):
   // blocks map onto items heaviest first within each XCD (xcd_remap_desc).
   int desc_order;
+  // Split-key forward for few queries per KV head (decode; see split_chunks):
+  // split_chunks chunks of split_keys keys per (sequence, KV head), whose
+  // partial rows (unnormalised O, running maximum and sum) go to `part`
+  // before a merge launch.  0: the regular forward.
+  int split_chunks, split_keys;
+  float* part;
 };
 
 // Query (0..31, within its 32-query row) at position p of a dS tile's key row:
@@ -188,6 +194,11 @@ struct DsStripe {
 int ds_stripes(const g4_problem& p, DsStripe* out, int max_out);
 // fp32 dK / dV sums of the row-striped backward (0 otherwise).
 size_t acc_bytes(const g4_problem& p);
+// Split-key forward: the number of key chunks per (sequence, KV head), 0 when
+// the problem takes the regular forward; *keys receives the keys per chunk.
+int split_chunks(const g4_problem& p, int* keys);
+// Workspace bytes of its partial rows (0 when not split).
+size_t split_bytes(const g4_problem& p);
 int64_t k_stream_tokens(const g4_problem& p);
 int64_t q_stream_tokens(const g4_problem& p);
 

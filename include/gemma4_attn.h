@@ -103,7 +103,11 @@ size_t g4_workspace_bytes(const g4_problem* p, int phase);
  *   fa4_local_varlen_forward   src/gemma4_fa4/h100.py:818-911 (+ h100_masks.py:62-152,
  *                              sparse schedule h100.py:490-601)
  *   global V-slab pairs        src/gemma4_fa4/h100.py:1148-1190, 1320-1387, 1013-1036
- * One launch covers the full Dv (no V slabs).
+ * One launch covers the full Dv (no V slabs).  Problems without key
+ * metadata whose query rows per KV head (query heads of a group x Sq) fit 32,
+ * over at least 256 keys (a decode step), split the keys into chunks over
+ * the GPU and merge the chunks' partial rows (kept in the workspace, which
+ * g4_workspace_bytes counts): two launches.
  */
 int g4_attn_fwd(const g4_problem* p,
                 const void* q, g4_layout q_layout,
