@@ -144,17 +144,33 @@ struct FwdKernel {
       }
   }
 
+  // AHEAD (double-buffered V, no key metadata): K runs two tiles ahead
+  // instead of one; K(it + 2) is issued into this step's K buffer once every
+  // wave is done reading it, so about two tiles of copies stay in flight (the
+  // split-key forward, whose steps are short next to a tile's fetch).  The
+  // caller issues K(0), V(0) and K(1) first.
+  template <bool AHEAD = false>
   __device__ __forceinline__ void step(int cur, int it, int ntiles, int t_first) {
+    static_assert(!AHEAD || (VDOUBLE && META == 0), "K-ahead steps");
     const int kb0 = (t_first + it) * BN;
     // This wave's copies of K (and, double-buffered, V) for this tile have
     // landed; the barrier publishes every wave's copies and ends all reads of
-    // the buffers refilled below.
-    if constexpr (VDOUBLE)
+    // the buffers refilled below.  (AHEAD: K(it + 1), issued last, may still
+    // be in flight.)
+    if constexpr (AHEAD) {
+      if (it + 1 < ntiles)
+        vm_wait<C::kLoadsPerWave>();
+      else
+        vm_wait<0>();
+    } else if constexpr (VDOUBLE) {
       vm_wait<0>();
-    else
+    } else {
       vm_wait<C::kLoadsPerWave>();
+    }
     barrier_lds();
-    if (it + 1 < ntiles) {
+    if constexpr (AHEAD) {
+      if (it + 1 < ntiles) issue_v(kb0 + BN, cur ^ 1);
+    } else if (it + 1 < ntiles) {
       issue_k(kb0 + BN, cur ^ 1);
       if (has_meta && wave == 0) issue_meta(*p, sq, kb0 + BN, smem + C::kLdsMeta + (cur ^ 1) * 512, lane, has_vid, has_doc);
       if constexpr (VDOUBLE) issue_v(kb0 + BN, cur ^ 1);
@@ -209,6 +225,11 @@ struct FwdKernel {
     } else if constexpr (!VDOUBLE) {
       vm_wait<C::kLoadsPerWave>();
       barrier_lds();
+    }
+    if constexpr (AHEAD) {
+      // every wave is done reading K(it): after the partial exchange's
+      // barrier, or with one wave, once its own S chain has its operands
+      if (it + 2 < ntiles) issue_k(kb0 + 2 * BN, cur);
     }
 
     // Mask (only on tiles the mask does not fully admit), then online softmax
@@ -608,12 +629,13 @@ __global__ void __launch_bounds__(D / 4, (D == 256 ? 2 : 1)) fwd_split_kernel(Fw
   if (ntiles > 0) {
     ker.issue_k(t_first * BN, 0);
     ker.issue_v(t_first * BN, 0);
+    if (ntiles > 1) ker.issue_k((t_first + 1) * BN, 1);
   }
 #pragma unroll
   for (int b = 0; b < K::kNB; ++b) ker.o_acc[b] = f32x16{};
   ker.m_run = kNegInf;
   ker.l_run = 0.f;
-  for (int it = 0; it < ntiles; ++it) ker.step(it & 1, it, ntiles, t_first);
+  for (int it = 0; it < ntiles; ++it) ker.template step<true>(it & 1, it, ntiles, t_first);
 
   // ---- partial rows ---------------------------------------------------------
   const float l_tot = ker.l_run + wave_xor32(ker.l_run);
@@ -636,10 +658,16 @@ __global__ void __launch_bounds__(D / 4, (D == 256 ? 2 : 1)) fwd_split_kernel(Fw
   }
 }
 
-// One 64-lane workgroup per (sequence, KV head, row): the chunks in order.
+// One workgroup per (sequence, KV head, row): the row's maximum over its
+// chunks first, then wave w sums chunks w, w + 4, ... (four chunks' loads in
+// flight per lane), and wave 0 adds the four waves' sums in order.  (One
+// 64-lane workgroup walking the chunks one by one took 73 us at 128 chunks.)
 template <int D>
-__global__ void __launch_bounds__(64) merge_split_kernel(FwdParams a) {
+__global__ void __launch_bounds__(256) merge_split_kernel(FwdParams a) {
   constexpr int E = D / 64;  // elements per lane: 4 (D = 256) or 8 (D = 512)
+  constexpr int kW = 4;      // waves
+  __shared__ float red_m[kW], red_l[kW];
+  __shared__ float stage[kW - 1][E][64];
   const g4_problem& p = a.p;
   const int grp = p.num_q_heads / p.num_kv_heads;
   const int rows = grp * p.seqlen_q;
@@ -649,22 +677,28 @@ __global__ void __launch_bounds__(64) merge_split_kernel(FwdParams a) {
   const Seq sq = resolve_seq(p, s);
   if (r >= grp * sq.lq) return;
   const int qh = kvh * grp + r / sq.lq, qi = r % sq.lq;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float* ml = a.part + (int64_t)p.num_seqs * p.num_kv_heads * n * rows * D;
   const int64_t row0 = (int64_t)g * n * rows + r;  // chunk c: row0 + c * rows
   float mx = kNegInf;
-  for (int c = 0; c < n; ++c) {
+  for (int c = threadIdx.x; c < n; c += kW * 64) {
     const float* e = ml + (row0 + (int64_t)c * rows) * 2;
     if (e[1] > 0.f) mx = fmaxf(mx, e[0]);
   }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (lane == 0) red_m[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
   float acc[E] = {};
   float l = 0.f;
-  for (int c = 0; c < n; ++c) {
+#pragma unroll 4
+  for (int c = wave; c < n; c += kW) {
     const int64_t row = row0 + (int64_t)c * rows;
-    const float* e = ml + row * 2;
-    if (!(e[1] > 0.f)) continue;
-    const float w = fast_exp2(e[0] - mx);
-    l += w * e[1];
+    const float lc = ml[row * 2 + 1];
+    // an empty chunk (no keys for this row) wrote l = 0 and O = 0
+    const float w = lc > 0.f ? fast_exp2(ml[row * 2] - mx) : 0.f;
+    l += w * lc;
     const float* po = a.part + row * D;
 #pragma unroll
     for (int h = 0; h < E / 4; ++h) {
@@ -672,6 +706,19 @@ __global__ void __launch_bounds__(64) merge_split_kernel(FwdParams a) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) acc[4 * h + u] += w * x[u];
     }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) stage[wave - 1][e][lane] = acc[e];
+    if (lane == 0) red_l[wave] = l;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 1; w < kW; ++w) {
+    l += red_l[w];
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] += stage[w - 1][e][lane];
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   __bf16* orow = a.o + tok_off(sq, s, sq.qtok, qi, a.ol) + (int64_t)qh * a.ol.head_stride;
@@ -699,7 +746,7 @@ static hipError_t launch_fwd_split(const FwdParams& a, hipStream_t stream) {
                      stream, a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(merge_split_kernel<D>, dim3((unsigned)(groups * rows)), dim3(64), 0, stream,
+  hipLaunchKernelGGL(merge_split_kernel<D>, dim3((unsigned)(groups * rows)), dim3(256), 0, stream,
                      a);
   return hipGetLastError();
 }
