@@ -6,7 +6,8 @@ stage takes the product over stored tiles for query tiles that stay inside
 their band and recomputes the others.  A 1500-token vision block starting
 past the first window reaches beyond the band of its first rows (those query
 tiles are recomputed) but not of its later rows; documents are added on a
-second segment.  Compared with the fp64 oracle through the C ABI stages.
+second segment.  Compared with the fp64 oracle through the C ABI stages, and the
+stages repeated on one workspace against their first results.
 """
 
 import pytest
@@ -52,3 +53,48 @@ def test_long_vision_block_reaches_past_the_band():
     check_forward(st.o, st.lse, o.cpu(), lse.cpu(), local=True, label="band")
     check_gradients([st.dq, st.dk, st.dv], [x.cpu() for x in (dq, dk, dv)],
                     [x.cpu() for x in (bq, bk, bv)], label="band")
+    # Stages repeated on one workspace (no delta pass between them, which is
+    # what zeroes the queue counters): each launch leaves its work-queue
+    # counters at zero, so the repeats visit every item again, bit for bit.
+    first = [t.clone() for t in (st.dq, st.dk, st.dv)]
+    st.dq.fill_(float("nan"))
+    st.dq_stage()
+    st.dq_stage()
+    st.dk.fill_(float("nan"))
+    st.dkdv()
+    torch.cuda.synchronize()
+    for a, b in zip((st.dq, st.dk, st.dv), first):
+        assert torch.equal(a, b)
+
+
+def test_work_queue_stages_repeat_on_one_workspace():
+    # 71 query tiles x 16 head pairs = 1136 items: the persistent work-queue
+    # launches (per-XCD runs for the stored-dS dQ).  Repeated without the delta
+    # pass, each launch must find its counters at zero and redo every item.
+    import gemma4_fa4_amd as g
+    from gemma4_fa4_amd import ops
+    from gemma4_fa4_amd.attention import _packed_plan
+
+    lens = [6000, 3000]
+    t = sum(lens)
+    q, k, v, do, dlse = qkv(778, t, t, 32, 16, 256)
+    c = cu(lens)
+    plan = _packed_plan(q.to(DEV), k.to(DEV), c.to(DEV), c.to(DEV), max(lens), max(lens),
+                        g.SLIDING_ATTENTION)
+    st = ops.Stages(plan, q.to(DEV), k.to(DEV), v.to(DEV), do.to(DEV), dlse.to(DEV))
+    print("work-queue stages repeated, local T=9000", flush=True)
+    st.forward()
+    st.delta()
+    st.dkdv()
+    st.dq_stage()
+    torch.cuda.synchronize()
+    first = [x.clone() for x in (st.dq, st.dk, st.dv)]
+    for _ in range(2):
+        st.dq.fill_(float("nan"))
+        st.dk.fill_(float("nan"))
+        st.dv.fill_(float("nan"))
+        st.dkdv()
+        st.dq_stage()
+        torch.cuda.synchronize()
+        for a, b in zip((st.dq, st.dk, st.dv), first):
+            assert torch.equal(a, b)
