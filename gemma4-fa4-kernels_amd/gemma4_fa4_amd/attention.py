@@ -536,6 +536,9 @@ class _Plan:
     global_backward: bool = False
     # Cumulative-array checks still to run before the first launch.
     pending: _CumulativeCheck | None = field(default=None, repr=False, compare=False)
+    # Workspace sizes already asked of the library, by (phase, ds_budget): the
+    # geometry above is fixed once the plan is made, the dS budget is not.
+    _ws_sizes: dict = field(default_factory=dict, repr=False, compare=False)
 
     def _settle(self) -> None:
         pending, self.pending = self.pending, None
@@ -573,13 +576,18 @@ class _Plan:
         return (self.num_seqs, self.num_q_heads, self.seqlen_q)
 
     def workspace_bytes(self, phase: int, prob: G4Problem | None = None) -> int:
+        key = (phase, self.ds_budget)
+        nbytes = self._ws_sizes.get(key)
+        if nbytes is not None:
+            return nbytes
         lib = _lib.load()
         if prob is None:
             prob = self.problem()
-        nbytes = lib.g4_workspace_bytes(ctypes.byref(prob), phase)
+        nbytes = int(lib.g4_workspace_bytes(ctypes.byref(prob), phase))
         if nbytes == 0 and lib.g4_last_error():
             _lib.check(_lib.G4_ERR_INVALID)
-        return int(nbytes)
+        self._ws_sizes[key] = nbytes
+        return nbytes
 
     def _workspace(self, phase: int, device, prob: G4Problem | None = None) -> torch.Tensor:
         nbytes = max(self.workspace_bytes(phase, prob), 256)
@@ -713,20 +721,26 @@ def _free_hbm(device) -> int:
     return free
 
 
-def _preflight_metadata_workspace(plan: _Plan, device) -> None:
-    # The forward's workspace: the vision-span tables (and raise flags).  The
-    # backward's delta and dS tiles are budgeted by _preflight_backward.
+def _preflight_metadata_workspace(plan: _Plan, device, free: int | None = None) -> int:
+    """The forward's workspace (vision-span tables, raise flags) against free HBM.
+
+    The backward's delta and dS tiles are budgeted by _preflight_backward.  Returns
+    the free-HBM reading it used (``free`` when given), so a backward fit made in
+    the same call reuses it instead of querying the device again.
+    """
     required = plan.workspace_bytes(0)
     if required > _METADATA_WORKSPACE_MAX_BYTES:
         raise UnsupportedMI355XPath(
             f"vision-span workspace requires {required} bytes, above the 2 GiB safety limit"
         )
-    free = _free_hbm(device)
+    if free is None:
+        free = _free_hbm(device)
     if required > free // 10:
         raise UnsupportedMI355XPath(
             f"vision-span workspace requires {required} bytes, exceeding the 10% free-HBM "
             f"budget of {free // 10} bytes ({free} bytes free)"
         )
+    return free
 
 
 def _global_backward_budget(free_bytes: int) -> int:
@@ -813,10 +827,10 @@ def _preflight_backward(plan: _Plan, q, k, v) -> None:
     _check_global_backward_budget(required, free)
 
 
-def _fit_local_backward(plan: _Plan, q, k, v) -> None:
+def _fit_local_backward(plan: _Plan, q, k, v, free: int | None = None) -> None:
     # The local backward has no budget error in the reference (FA4's autograd
     # allocates what it needs); its stored-dS band just shrinks to what fits.
-    _fit_or_pin(plan, q, k, v, _free_hbm(q.device))
+    _fit_or_pin(plan, q, k, v, _free_hbm(q.device) if free is None else free)
 
 
 def _refit_backward(plan: _Plan, q, k, v) -> None:
@@ -895,9 +909,9 @@ def fa4_local_forward(
     _validate_local_bshd(q, k, v, spec)
     ids = _prepare_vision_block_ids(vision_block_ids, q)
     plan = _fixed_plan(q, k, spec, vision=ids)
-    _preflight_metadata_workspace(plan, q.device)
+    free = _preflight_metadata_workspace(plan, q.device)  # one reading for both checks
     if _requires_backward(q, k, v):
-        _fit_local_backward(plan, q, k, v)
+        _fit_local_backward(plan, q, k, v, free)
     return _run(q, k, v, plan)
 
 
@@ -931,10 +945,11 @@ def fa4_local_varlen_forward(
             q, k, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, spec,
             vision=vision, documents=documents,
         )
+        free = None  # one free-HBM reading for both checks of this call
         if vision is not None:
-            _preflight_metadata_workspace(plan, q.device)
+            free = _preflight_metadata_workspace(plan, q.device)
         if _requires_backward(q, k, v):
-            _fit_local_backward(plan, q, k, v)
+            _fit_local_backward(plan, q, k, v, free)
         return plan
 
     return _run_checked(q, k, v, check, prepare)
