@@ -1649,7 +1649,9 @@ struct DqDsKernel {
     const int row0 = kt * C::kBN;
     kcp.issue_clamped(kbase + row0 * kstride, kstride, min(C::kBN, sq.lk - row0),
                       smem + C::kLdsK + buf * C::kKTile);
-    // dS: four 4 KB tiles per head, two 1 KB chunks per wave and head.
+    // dS: four 4 KB tiles per head, two 1 KB chunks per wave and head, each
+    // read once (non-temporal: the K tiles stay in the L2 for the other
+    // workgroups of the band; config 5 dQ -3%, config 3 -7%, results the same).
     const int g = wave >> 1;
     if (kt >= lo_copy && kt <= hi_copy) {
       const char* src = ds_copy_row + (int64_t)(kt - lo_copy) * ds_col_stride;
@@ -1660,8 +1662,8 @@ struct DqDsKernel {
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             const int chunk = (wave & 1) * 2 + c;
-            b2l16(src + h * ds_head_stride, (uint32_t)(chunk * 1024 + lane * 16),
-                  dst + chunk * 1024);
+            b2l16_nt(src + h * ds_head_stride, (uint32_t)(chunk * 1024 + lane * 16),
+                     dst + chunk * 1024);
           }
         }
       }
@@ -1925,7 +1927,7 @@ __device__ __forceinline__ void dq_ds_item(const BwdParams& a, char* smem_raw, i
             *(const bf16x8 G4_LDS*)(stage + (r * C::kCPR + (c ^ (r & (C::kCPR - 1)))) * 16);
         __bf16* row =
             a.dq + tok_off(sq, s, sq.qtok, my_i, a.dql) + (int64_t)(qh + h) * a.dql.head_stride;
-        *(bf16x8*)(row + c * 8) = v;
+        __builtin_nontemporal_store(v, (bf16x8*)(row + c * 8));  // (written once)
       }
     }
   }

@@ -121,6 +121,17 @@ __device__ __forceinline__ void b2l16(const void* base, uint32_t voff, char G4_L
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (void G4_LDS*)lds_wave_base, 16, voff, 0, 0, 0);
 }
 
+// The same copy with the non-temporal cache policy (nt): for data read once
+// (the stored dS tiles), so the stream does not push operands that other
+// workgroups re-read out of the L2.
+__device__ __forceinline__ void b2l16_nt(const void* base, uint32_t voff,
+                                         char G4_LDS* lds_wave_base) {
+  __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (void G4_LDS*)lds_wave_base, 16, voff, 0, 0,
+                                           /*nt=*/2);
+}
+
 // Async 4-byte global -> LDS copy: lane l writes LDS bytes [lds_wave_base +
 // 4 l, +4) from base + voff (a uniform base, a 32-bit per-lane byte offset).
 // Through a buffer descriptor rather than a global address: the compiler
