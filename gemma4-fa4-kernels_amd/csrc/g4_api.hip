@@ -180,7 +180,7 @@ int fwd_impl(const g4_problem* p, const void* q, g4_layout ql, const void* k, g4
   a.ol = ol;
   a.num_seqs = p->num_seqs;
   if (g4::spans_bytes(*p)) {
-    hipError_t e = g4::launch_spans(*p, ws, st);
+    hipError_t e = g4::launch_spans(*p, ws, st, /*query_reach=*/false);  // (span_hi only)
     if (e != hipSuccess) return hip_fail(e, "span table");
   }
   g4::span_arrays(*p, ws, &a.span_lo, &a.span_hi);

@@ -15,7 +15,7 @@ struct FwdParams {
   __bf16* o;
   float* lse;
   g4_layout ql, kl, vl, ol;
-  const int* span_lo;  // per K-stream token: first position of its vision span (or itself)
+  const int* span_lo;  // per K-stream token: first query position reaching it (see g4_meta.hip)
   const int* span_hi;  // per K-stream token: last position of its vision span (or itself)
   int num_seqs;
   int ntq;             // query tiles per sequence (set by the launcher)
@@ -202,7 +202,10 @@ size_t split_bytes(const g4_problem& p);
 int64_t k_stream_tokens(const g4_problem& p);
 int64_t q_stream_tokens(const g4_problem& p);
 
-hipError_t launch_spans(const g4_problem& p, void* ws, hipStream_t stream);
+// query_reach: span_lo as the first query reaching each key (backward, tile
+// scheduler); without it span_lo keeps each key's own span start (the forward
+// reads only span_hi).
+hipError_t launch_spans(const g4_problem& p, void* ws, hipStream_t stream, bool query_reach = true);
 void span_arrays(const g4_problem& p, void* ws, const int** lo, const int** hi);
 hipError_t launch_fwd(const FwdParams& a, hipStream_t stream);
 hipError_t launch_bwd_delta(const BwdParams& a, hipStream_t stream);

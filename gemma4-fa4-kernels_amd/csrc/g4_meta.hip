@@ -3,12 +3,19 @@
 // Vision span of a K-stream token t with vision ID >= 0: the first and last
 // position, within t's sequence, of the tokens sharing t's (document, vision)
 // pair.  For the local Gemma mask a query at position a may attend future keys
-// only inside its span (no right window cap), and a key at position j may be
-// attended by earlier queries only inside its span, so the spans bound the
-// key range of a query tile and the query range of a key tile exactly, for
-// any ID pattern (repeated or non-contiguous IDs included).  They are computed
-// on device with one open-addressing hash table per sequence (2 * Lk slots),
-// O(tokens), no host round trip.
+// only inside its span (no right window cap), so the span ends bound the key
+// range of a query tile (span_hi, any ID pattern, repeated or non-contiguous
+// IDs included).  They are computed on device with one open-addressing hash
+// table per sequence (2 * Lk slots), O(tokens), no host round trip.
+//
+// The query range of a key tile is bounded below by span_lo, which for the
+// backward and the tile scheduler (not the forward, which does not read it)
+// is the first query position whose reach (its position, or its span end)
+// is at or past the key: then a key tile's query range holds every query tile
+// whose key range holds the key tile.  The stored-dS dQ pass reads, per query
+// row, every band tile up to the row's furthest reach, so the dK/dV pass must
+// write each of them (zeros where no query of the row attends the tile: the
+// keys between the runs of a vision ID that repeats non-contiguously).
 #include "g4_kernels.h"
 
 namespace g4 {
@@ -133,6 +140,114 @@ __global__ void span_lookup_kernel(g4_problem p, SpanWs w, int64_t tk) {
   }
 }
 
+// span_lo[j] = min{a >= off : M(a) >= j}, with M(a) the largest span end of
+// the query positions off..a (each at least the position itself) and off =
+// Sk - Sq the first query position.  Never above the key's own span start, so
+// it only widens the query ranges of key tiles.  M comes from one prefix
+// maximum over the whole K stream of g(t) = ks + span_hi[t] for query
+// positions (ks the first token of t's sequence) and -1 for the others:
+// every value from an earlier sequence lies below ks, so no reset is needed
+// at sequence starts, and M(a) = G(ks + a) - ks.  The scan runs in chunks of
+// kReachChunk tokens: one pass writes each chunk's maximum, the next scans
+// each chunk from the maxima of the earlier chunks of its first sequence.  M
+// is written over the hash table's `first` words and the chunk maxima over
+// its `last` words (both free once the spans are looked up); then one binary
+// search per key over its sequence's M, which is non-decreasing and ends at
+// M(Sk - 1) = Sk - 1.
+constexpr int kReachChunk = 1024;  // tokens per workgroup, one per thread
+
+__device__ __forceinline__ long long reach_end(const g4_problem& p, SpanWs w, int64_t t,
+                                               int64_t tk) {
+  if (t >= tk) return -1;
+  int s, lk;
+  int64_t ks;
+  seq_of_token(p, t, s, ks, lk);
+  const int lq = resolve_seq(p, s).lq;
+  return (int)(t - ks) >= lk - lq ? (long long)ks + w.hi[t] : -1;
+}
+
+__device__ __forceinline__ long long wave_max(long long v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__global__ void __launch_bounds__(kReachChunk) span_chunk_max_kernel(g4_problem p, SpanWs w,
+                                                                     int64_t tk) {
+  __shared__ long long wmax[kReachChunk / 64];
+  const int tid = threadIdx.x;
+  const long long v = wave_max(reach_end(p, w, blockIdx.x * (int64_t)kReachChunk + tid, tk));
+  if ((tid & 63) == 0) wmax[tid >> 6] = v;
+  __syncthreads();
+  if (tid == 0) {
+    long long all = -1;
+    for (int x = 0; x < kReachChunk / 64; ++x) all = max(all, wmax[x]);
+    reinterpret_cast<long long*>(w.last)[blockIdx.x] = all;
+  }
+}
+
+__global__ void __launch_bounds__(kReachChunk) span_chunk_scan_kernel(g4_problem p, SpanWs w,
+                                                                      int64_t tk) {
+  __shared__ long long wtot[kReachChunk / 64], wcarry[kReachChunk / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = blockIdx.x * (int64_t)kReachChunk, t = t0 + tid;
+  // Earlier chunks that can hold tokens of this chunk's sequences: from the
+  // one holding the first token's sequence start.
+  int s0, lk0;
+  int64_t ks0;
+  seq_of_token(p, t0, s0, ks0, lk0);
+  const long long* cmax = reinterpret_cast<const long long*>(w.last);
+  long long c = -1;
+  for (int64_t x = ks0 / kReachChunk + tid; x < (int64_t)blockIdx.x; x += kReachChunk)
+    c = max(c, cmax[x]);
+  c = wave_max(c);
+  long long v = reach_end(p, w, t, tk);
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const long long u = __shfl_up(v, o, 64);
+    if (lane >= o) v = max(v, u);
+  }
+  if (lane == 63) wtot[wave] = v;
+  if (lane == 0) wcarry[wave] = c;
+  __syncthreads();
+#pragma unroll
+  for (int x = 0; x < kReachChunk / 64; ++x) {
+    v = max(v, wcarry[x]);
+    if (x < wave) v = max(v, wtot[x]);
+  }
+  if (t < tk) {
+    int s, lk;
+    int64_t ks;
+    seq_of_token(p, t, s, ks, lk);
+    w.first[t] = v >= ks ? (int)(v - ks) : -1;  // -1: no query position yet
+  }
+}
+
+__global__ void span_reach_kernel(g4_problem p, SpanWs w, int64_t tk) {
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < tk;
+       t += (int64_t)gridDim.x * blockDim.x) {
+    int s, lk;
+    int64_t ks;
+    seq_of_token(p, t, s, ks, lk);
+    const Seq sq = resolve_seq(p, s);
+    if (sq.lq <= 0) {
+      w.lo[t] = 0x7fffffff;  // no query attends this sequence's keys
+      continue;
+    }
+    const int j = (int)(t - ks);
+    const int* m = w.first + ks;
+    int l = max(lk - sq.lq, 0), r = lk - 1;  // the first a in [off, Sk) with M(a) >= j
+    while (l < r) {
+      const int mid = (l + r) >> 1;
+      if (m[mid] >= j)
+        r = mid;
+      else
+        l = mid + 1;
+    }
+    w.lo[t] = l;
+  }
+}
+
 __global__ void mask_kernel(g4_problem p, uint8_t* out) {
   const int64_t per_seq = (int64_t)p.seqlen_q * p.seqlen_k;
   const int64_t n = per_seq * p.num_seqs;
@@ -212,12 +327,18 @@ size_t spans_bytes(const g4_problem& p) {
   return align256(tk * 4) * 2 + align256(2 * tk * 8) + align256(2 * tk * 4) * 2;
 }
 
-hipError_t launch_spans(const g4_problem& p, void* ws, hipStream_t stream) {
+hipError_t launch_spans(const g4_problem& p, void* ws, hipStream_t stream, bool query_reach) {
   int64_t tk = k_stream_tokens(p);
   SpanWs w = span_ws(ws, tk);
   span_init_kernel<<<grid_for(2 * tk, 256), 256, 0, stream>>>(w, 2 * tk);
   span_insert_kernel<<<grid_for(tk, 256), 256, 0, stream>>>(p, w, tk);
   span_lookup_kernel<<<grid_for(tk, 256), 256, 0, stream>>>(p, w, tk);
+  if (query_reach && tk > 0) {
+    const int64_t chunks = (tk + kReachChunk - 1) / kReachChunk;
+    span_chunk_max_kernel<<<chunks, kReachChunk, 0, stream>>>(p, w, tk);
+    span_chunk_scan_kernel<<<chunks, kReachChunk, 0, stream>>>(p, w, tk);
+    span_reach_kernel<<<grid_for(tk, 256), 256, 0, stream>>>(p, w, tk);
+  }
   return hipGetLastError();
 }
 

@@ -98,3 +98,46 @@ def test_work_queue_stages_repeat_on_one_workspace():
         torch.cuda.synchronize()
         for a, b in zip((st.dq, st.dk, st.dv), first):
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("poison", [0xFF, 0x7F])
+def test_repeated_vision_id_with_a_gap_and_a_poisoned_workspace(poison):
+    """A vision ID in two runs with another block between them (queries shorter
+    than keys, three packed sequences).  Queries of the first run attend the
+    second, so the stored-dS dQ pass reads every band tile up to the second
+    run's end for their rows, including the tiles of the block between the
+    runs, which those queries do not attend: the dK/dV pass must write them
+    (zeros).  The workspace is filled with NaN (0xFF) or large finite (0x7F)
+    bytes first, so a tile read without being written shows in dQ."""
+    import gemma4_fa4_amd as g
+    from gemma4_fa4_amd import ops
+    from gemma4_fa4_amd.attention import _packed_plan
+
+    lq, lk = [354, 7, 333], [549, 407, 727]
+    q, k, v, do, dlse = qkv(5291, sum(lq), sum(lk), 4, 2, 256)
+    vis = torch.full((sum(lk),), -1, dtype=torch.int32)
+    s2 = lk[0] + lk[1]            # third sequence: queries at key positions 394..726
+    vis[s2 + 399:s2 + 440] = 0
+    vis[s2 + 440:s2 + 501] = 1    # first run of ID 1
+    vis[s2 + 501:s2 + 642] = 2    # the block between the runs
+    vis[s2 + 642:s2 + 716] = 1    # second run of ID 1
+    vis[100:180] = 3              # and one ordinary block in the first sequence
+    cq, ck = cu(lq), cu(lk)
+    plan = _packed_plan(q.to(DEV), k.to(DEV), cq.to(DEV), ck.to(DEV), max(lq), max(lk),
+                        g.SLIDING_ATTENTION, vision=vis.to(DEV))
+    st = ops.Stages(plan, q.to(DEV), k.to(DEV), v.to(DEV), do.to(DEV), dlse.to(DEV))
+    print(f"repeated vision ID, workspace filled with {poison:#x}", flush=True)
+    st.ws.fill_(poison)
+    st.forward()
+    st.backward()
+    torch.cuda.synchronize()
+    args = dict(sliding_window=1024, vision_block_ids=vis.to(DEV), allow_vision_bidirectional=True)
+    o, lse, dq, dk, dv = attention_fwd_bwd(
+        q.to(DEV), k.to(DEV), v.to(DEV), cq.tolist(), ck.tolist(), do=do.to(DEV),
+        dlse=dlse.to(DEV), compute_dtype=torch.float64, **args)
+    _, bq, bk, bv = bf16_baseline_fwd_bwd(
+        q.to(DEV), k.to(DEV), v.to(DEV), cq.tolist(), ck.tolist(), do=do.to(DEV),
+        dlse=dlse.to(DEV), **args)
+    check_forward(st.o, st.lse, o.cpu(), lse.cpu(), local=True, label="repeated id")
+    check_gradients([st.dq, st.dk, st.dv], [x.cpu() for x in (dq, dk, dv)],
+                    [x.cpu() for x in (bq, bk, bv)], label="repeated id")
