@@ -5,7 +5,8 @@ layout, 1-5 sequences of random query and key lengths (queries the lower-right
 suffix of their keys, including empty and one-token sequences), and for head
 dim 256 random vision blocks and documents, sometimes a decode shape (a few
 queries over many keys: the split-key forward) and sometimes a small dS
-budget (striped or recompute backward).  The forward and the whole backward
+budget (striped or recompute backward).  The workspace and the outputs start
+filled with NaN or large finite bytes.  The forward and the whole backward
 (g4_attn_bwd) are checked against the fp64 oracle with the M1 envelopes.  The
 cases are fixed by their seeds; the sweep exists to reach combinations the
 targeted tests do not list one by one.
@@ -60,6 +61,8 @@ def _draw(seed):
     budget = 0
     if d == 512 and not decode and rng.integers(0, 3) == 0:
         budget = int(rng.choice([-1, 4 << 20, 16 << 20]))
+    elif d == 256 and not decode and rng.integers(0, 4) == 0:
+        budget = -1  # no stored dS band: the dQ stage recomputes S and dP
     return dict(d=d, hq=hq, hkv=hkv, packed=packed, lq=lq, lk=lk, window=window, vis=vis,
                 docs=docs, budget=budget)
 
@@ -91,6 +94,11 @@ def test_random_problem_matches_the_oracle(seed):
         args = [t.view(b, t.shape[0] // b, *t.shape[1:]).to(DEV) for t in (q, k, v, do)]
         dl = dlse.view(hq, b, -1).permute(1, 0, 2).contiguous().to(DEV)
     st = ops.Stages(plan, *args, dl)
+    # The workspace and the outputs are uninitialised memory for the library:
+    # fill them with NaN (0xFF) or large finite (0x7F) bytes, so a value read
+    # before it is written, or an output element never written, shows.
+    for t in (st.ws, st.o, st.lse, st.dq, st.dk, st.dv):
+        t.view(torch.uint8).fill_(0xFF if seed % 2 else 0x7F)
     st.forward()
     st.backward()
     torch.cuda.synchronize()
