@@ -81,6 +81,35 @@ def _check_ranges(ranges_q, ranges_k, allowed, row_tile_q, row_tile_k, tight):
             assert lo <= qs.min() and qs.max() < hi, (t, lo, hi, qs.min(), qs.max())
 
 
+def _reach(vision, docs, n):
+    """Each position's furthest key: its own position, or the last position of
+    its (document, vision ID) pair."""
+    reach = np.arange(n)
+    if vision is not None:
+        v = vision.numpy()
+        d = docs.numpy() if docs is not None else np.zeros(n, dtype=np.int64)
+        last = {}
+        for a in range(n):
+            if v[a] >= 0:
+                last[(int(d[a]), int(v[a]))] = a
+        for a in range(n):
+            if v[a] >= 0:
+                reach[a] = max(a, last[(int(d[a]), int(v[a]))])
+    return reach
+
+
+def _check_key_ranges_hold_band_rows(ranges_k, reach, window, row_tile_k):
+    """A query row's stored-dS band runs over the key tiles from its window
+    start to its reach, and the dQ pass reads all of them, so each of those key
+    tiles must hold the row in its query range (the dK/dV pass then writes the
+    tile, zeros where the row attends none of its keys)."""
+    for a in range(len(reach)):
+        t0 = max(0, a - window + 1) // row_tile_k if window else 0
+        for t in range(t0, reach[a] // row_tile_k + 1):
+            lo, hi = ranges_k[t]
+            assert lo <= a < hi, (a, t, lo, hi)
+
+
 @pytest.mark.parametrize("seed,length,nblk,window,with_doc", [
     (0, 1500, 3, 1024, False), (1, 3000, 4, 1024, False), (2, 777, 2, 100, True),
     (3, 2600, 5, 1024, False), (4, 4096, 0, 1024, False), (5, 4096, 0, None, False),
@@ -100,6 +129,7 @@ def test_device_scheduler_ranges_cover_the_mask(seed, length, nblk, window, with
     rk = ops.tile_ranges(plan, 1, 64, DEV).cpu()[0].tolist()
     allowed = _oracle_mask(length, length, window, vision, docs).numpy()
     _check_ranges(rq, rk, allowed, 128, 64, tight=docs is None)
+    _check_key_ranges_hold_band_rows(rk, _reach(vision, docs, length), window, 64)
 
 
 def test_device_scheduler_handles_repeated_noncontiguous_ids():
@@ -116,3 +146,6 @@ def test_device_scheduler_handles_repeated_noncontiguous_ids():
     allowed = _oracle_mask(length, length, 1024, vision, None).numpy()
     _check_ranges(rq, rk, allowed, 128, 64, tight=True)
     assert rq[0][1] == 510  # query 10 reaches key 509
+    # Key tiles between the two runs of ID 4 hold the first run's rows.
+    _check_key_ranges_hold_band_rows(rk, _reach(vision, None, length), 1024, 64)
+    assert rk[5][0] <= 10
