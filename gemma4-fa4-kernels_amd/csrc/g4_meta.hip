@@ -30,6 +30,7 @@ struct SpanWs {
   unsigned long long* keys;
   int* first;
   int* last;
+  int* repeats;  // nonzero when some (document, vision ID) key has two runs
 };
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -46,6 +47,8 @@ __host__ __device__ inline SpanWs span_ws(void* ws, int64_t tk) {
   w.first = (int*)b;
   b += align256(2 * tk * 4);
   w.last = (int*)b;
+  b += align256(2 * tk * 4);
+  w.repeats = (int*)b;
   return w;
 }
 
@@ -86,6 +89,7 @@ __device__ inline int64_t probe_slot(SpanWs w, int64_t base, int64_t cap, unsign
 }
 
 __global__ void span_init_kernel(SpanWs w, int64_t nslots) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *w.repeats = 0;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nslots;
        i += (int64_t)gridDim.x * blockDim.x) {
     w.keys[i] = kEmpty;
@@ -129,10 +133,13 @@ __global__ void span_lookup_kernel(g4_problem p, SpanWs w, int64_t tk) {
     int vid = p.vision_ids[t];
     int lo = j, hi = j;
     if (vid >= 0) {
-      int64_t slot = probe_slot(w, 2 * ks, 2 * (int64_t)lk, span_key(p, t, vid), false);
+      const unsigned long long key = span_key(p, t, vid);
+      int64_t slot = probe_slot(w, 2 * ks, 2 * (int64_t)lk, key, false);
       if (slot >= 0) {
         lo = w.first[slot];
         hi = w.last[slot];
+        // A run that starts after its key's first position: the key repeats.
+        if (lo < j && span_key(p, t - 1, p.vision_ids[t - 1]) != key) atomicOr(w.repeats, 1);
       }
     }
     w.lo[t] = lo;
@@ -154,6 +161,12 @@ __global__ void span_lookup_kernel(g4_problem p, SpanWs w, int64_t tk) {
 // its `last` words (both free once the spans are looked up); then one binary
 // search per key over its sequence's M, which is non-decreasing and ends at
 // M(Sk - 1) = Sk - 1.
+//
+// When every (document, vision ID) key forms a single run (the lookup pass
+// sets `repeats` otherwise), a position's span ends inside its own run, so the
+// first position whose span reaches key j is j's span start, or Sk - Sq when
+// the span starts before the first query position: the span starts are then a
+// lower bound as good as the query reach, and the three passes return at once.
 constexpr int kReachChunk = 1024;  // tokens per workgroup, one per thread
 
 __device__ __forceinline__ long long reach_end(const g4_problem& p, SpanWs w, int64_t t,
@@ -175,6 +188,7 @@ __device__ __forceinline__ long long wave_max(long long v) {
 __global__ void __launch_bounds__(kReachChunk) span_chunk_max_kernel(g4_problem p, SpanWs w,
                                                                      int64_t tk) {
   __shared__ long long wmax[kReachChunk / 64];
+  if (*w.repeats == 0) return;  // span starts are the query reach (uniform)
   const int tid = threadIdx.x;
   const long long v = wave_max(reach_end(p, w, blockIdx.x * (int64_t)kReachChunk + tid, tk));
   if ((tid & 63) == 0) wmax[tid >> 6] = v;
@@ -189,6 +203,7 @@ __global__ void __launch_bounds__(kReachChunk) span_chunk_max_kernel(g4_problem 
 __global__ void __launch_bounds__(kReachChunk) span_chunk_scan_kernel(g4_problem p, SpanWs w,
                                                                       int64_t tk) {
   __shared__ long long wtot[kReachChunk / 64], wcarry[kReachChunk / 64];
+  if (*w.repeats == 0) return;  // (uniform)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = blockIdx.x * (int64_t)kReachChunk, t = t0 + tid;
   // Earlier chunks that can hold tokens of this chunk's sequences: from the
@@ -224,6 +239,7 @@ __global__ void __launch_bounds__(kReachChunk) span_chunk_scan_kernel(g4_problem
 }
 
 __global__ void span_reach_kernel(g4_problem p, SpanWs w, int64_t tk) {
+  if (*w.repeats == 0) return;  // span_lo keeps the span starts
   for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < tk;
        t += (int64_t)gridDim.x * blockDim.x) {
     int s, lk;
@@ -324,7 +340,7 @@ int64_t q_stream_tokens(const g4_problem& p) {
 size_t spans_bytes(const g4_problem& p) {
   if (p.vision_ids == nullptr || !p.bidirectional_vision) return 0;
   int64_t tk = k_stream_tokens(p);
-  return align256(tk * 4) * 2 + align256(2 * tk * 8) + align256(2 * tk * 4) * 2;
+  return align256(tk * 4) * 2 + align256(2 * tk * 8) + align256(2 * tk * 4) * 2 + 256;
 }
 
 hipError_t launch_spans(const g4_problem& p, void* ws, hipStream_t stream, bool query_reach) {
