@@ -479,8 +479,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): this build "
-              "runs the attention kernels on a single MI355X; see DESIGN.md for how the path "
-              "would shard across GPUs.", file=sys.stderr)
+              "runs the attention kernels on a single MI355X; sharding the path across GPUs "
+              "is designed but not built.", file=sys.stderr)
         return 2
 
     import torch
