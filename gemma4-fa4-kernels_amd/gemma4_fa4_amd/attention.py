@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+import time
 import weakref
 from dataclasses import dataclass, field
 
@@ -716,9 +717,37 @@ def _packed_plan(q, k, cu_q, cu_k, max_q, max_k, spec, *, vision=None, documents
 # ---------------------------------------------------------------------------
 
 
+# Free-HBM readings taken by _free_hbm, per torch device: (time, bytes, reader).
+_FREE_HBM_READINGS: dict[torch.device, tuple[float, int, object]] = {}
+# How long the checks made before a forward's first launch reuse a reading.
+_FREE_HBM_REUSE_S = 0.02
+
+
 def _free_hbm(device) -> int:
+    """Free HBM bytes on ``device`` now (hipMemGetInfo)."""
     free, _total = torch.cuda.mem_get_info(device)
+    _FREE_HBM_READINGS[device] = (time.monotonic(), free, _free_hbm)
     return free
+
+
+def _recent_free_hbm(device) -> int:
+    """Free HBM bytes read by ``_free_hbm`` within the last 20 ms, else read now.
+
+    hipMemGetInfo takes tens of microseconds once the device has gone idle,
+    and the forward-time checks run before the first launch, so a model whose
+    layers call the adapters back to back would pay it per layer with the GPU
+    waiting.  Those checks (metadata workspace, forward outputs, the
+    backward's preliminary dS fit and the global backward budget) take such
+    a recent reading instead.  A reading is reused only if the current
+    ``_free_hbm`` took it.  The backward's own fit (``_refit_backward``) always
+    reads afresh, so a forward admitted on a reading that has since gone stale
+    still fails closed, with the same typed error, before the backward
+    allocates.
+    """
+    entry = _FREE_HBM_READINGS.get(device)
+    if entry is not None and entry[2] is _free_hbm and time.monotonic() - entry[0] < _FREE_HBM_REUSE_S:
+        return entry[1]
+    return _free_hbm(device)
 
 
 def _preflight_metadata_workspace(plan: _Plan, device, free: int | None = None) -> int:
@@ -734,7 +763,7 @@ def _preflight_metadata_workspace(plan: _Plan, device, free: int | None = None) 
             f"vision-span workspace requires {required} bytes, above the 2 GiB safety limit"
         )
     if free is None:
-        free = _free_hbm(device)
+        free = _recent_free_hbm(device)
     if required > free // 10:
         raise UnsupportedMI355XPath(
             f"vision-span workspace requires {required} bytes, exceeding the 10% free-HBM "
@@ -822,7 +851,7 @@ def _fit_or_pin(plan: _Plan, q, k, v, free: int) -> int:
 
 def _preflight_backward(plan: _Plan, q, k, v) -> None:
     plan.global_backward = True
-    free = _free_hbm(q.device)
+    free = _recent_free_hbm(q.device)
     required = _fit_or_pin(plan, q, k, v, free)
     _check_global_backward_budget(required, free)
 
@@ -830,7 +859,7 @@ def _preflight_backward(plan: _Plan, q, k, v) -> None:
 def _fit_local_backward(plan: _Plan, q, k, v, free: int | None = None) -> None:
     # The local backward has no budget error in the reference (FA4's autograd
     # allocates what it needs); its stored-dS band just shrinks to what fits.
-    _fit_or_pin(plan, q, k, v, _free_hbm(q.device) if free is None else free)
+    _fit_or_pin(plan, q, k, v, _recent_free_hbm(q.device) if free is None else free)
 
 
 def _refit_backward(plan: _Plan, q, k, v) -> None:
@@ -855,7 +884,7 @@ def _preflight_forward_outputs(q: torch.Tensor) -> None:
     out_bytes = q.numel() * q.element_size()
     lse_bytes = q.numel() // q.shape[-1] * 4
     required = 2 * (out_bytes + lse_bytes)
-    free = _free_hbm(q.device)
+    free = _recent_free_hbm(q.device)
     if required > free * 8 // 10:
         raise UnsupportedMI355XPath(
             f"forward outputs require about {required} bytes, above 80% of the {free} "
