@@ -550,3 +550,30 @@ def test_row_preparation_validation_happens_before_any_launch():
                               0x6000, lay, 0x7000, lay, 0x8000, 0x9000, 1 << 20,
                               None) == _lib.G4_ERR_UNSUPPORTED
     assert b"head_dim 512" in lib.g4_last_error()
+
+
+def test_forward_checks_reuse_a_recent_free_hbm_reading(monkeypatch):
+    """The forward-time checks reuse a hipMemGetInfo reading for 20 ms; a
+    replaced ``_free_hbm`` is always consulted, and the backward's refit reads
+    afresh through ``_free_hbm`` itself."""
+    import time
+
+    calls = []
+
+    def mem_get_info(device):
+        calls.append(device)
+        return (1000 + len(calls), 2000)
+
+    monkeypatch.setattr(torch.cuda, "mem_get_info", mem_get_info)
+    monkeypatch.setattr(att, "_FREE_HBM_READINGS", {})
+    dev = torch.device("cuda", 0)
+    assert att._recent_free_hbm(dev) == 1001
+    assert att._recent_free_hbm(dev) == 1001 and len(calls) == 1  # reused
+    assert att._free_hbm(dev) == 1002  # always a fresh read (the backward's refit)
+    assert att._recent_free_hbm(dev) == 1002 and len(calls) == 2
+    monkeypatch.setattr(att, "_FREE_HBM_REUSE_S", 0.0)
+    time.sleep(0.001)
+    assert att._recent_free_hbm(dev) == 1003  # expired: read again
+    monkeypatch.setattr(att, "_FREE_HBM_REUSE_S", 60.0)
+    monkeypatch.setattr(att, "_free_hbm", lambda _d: 7)
+    assert att._recent_free_hbm(dev) == 7  # a replaced reader is never bypassed
