@@ -238,7 +238,10 @@ int g4_mask_materialize(const g4_problem* p, uint8_t* out,
  * (seq, tile of row_tile queries) the half-open range [k_lo, k_hi) of key
  * indices the forward and dQ kernels visit; direction 1: for each
  * (seq, tile of row_tile keys) the range [i_lo, i_hi) of query indices the
- * dK/dV kernel visits.  Indices are sequence-local.  Writes int32 pairs for
+ * dK/dV kernel visits: every query whose key range reaches the tile, so it
+ * can be wider than the tile's allowed pairs when a vision ID repeats with a
+ * gap (the dQ kernel reads the stored dS of all those tiles).  Indices are
+ * sequence-local.  Writes int32 pairs for
  * num_seqs * ceil(max_len / row_tile) rows (empty rows give lo == hi).
  * Replaces the host schedule build_gemma4_local_sparse_schedule
  * (src/gemma4_fa4/sparse_schedule.py:291-374) and its D2H/H2D copies
